@@ -1,0 +1,48 @@
+/*
+ * rdnattention_ext.h -- entry points of librdnattention.so that have no
+ * counterpart in the reference's C ABI.  They exist for testing and
+ * measurement; the four drop-in symbols in rdnattention.h do not depend on
+ * them.  Same return-code and error-string conventions as rdnattention.h.
+ */
+#ifndef RDNATTENTION_EXT_H
+#define RDNATTENTION_EXT_H
+
+#include "rdnattention.h"
+
+/* Kernel path for rdna_attention_forward_path(). */
+#define RDNA_PATH_AUTO 0    /* what rdna_attention_forward() picks */
+#define RDNA_PATH_PREFILL 1 /* tiled prefill kernel */
+#define RDNA_PATH_SPLITK 2  /* split-K decode kernel + combine */
+
+/* rdna_attention_forward() with the kernel path forced, so tests can run the
+ * prefill and split-K kernels on the same input.  No reference counterpart:
+ * for parity tests and benchmarks. */
+RDNA_API int32_t rdna_attention_forward_path(
+    const void* q, const void* k, const void* v, void* output,
+    const void* rot_cos, const void* rot_sin,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads,
+    uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
+    float scale, int32_t causal, int32_t has_rope, int32_t window_size,
+    int32_t path, void* hip_stream);
+
+/* Exact int32 scores S = Q_i8 K_i8^T (GQA head map kv = h / (Hq/Hkv)),
+ * written to `scores`, a contiguous int32 [batch, num_heads, seq_len,
+ * key_seq_len] device buffer.  Uses the same int8 MFMA tiles as
+ * rdna_attention_forward_int8qk's first GEMM.  No reference counterpart:
+ * it exposes the scores so tests can check them bit for bit. */
+RDNA_API int32_t rdna_int8_qk_scores(
+    const void* q, const void* k, int32_t* scores,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads,
+    uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
+    void* hip_stream);
+
+/* Library version string ("0.1.0-gfx950"). */
+RDNA_API const char* rdna_version(void);
+
+#endif /* RDNATTENTION_EXT_H */

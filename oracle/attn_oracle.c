@@ -262,8 +262,13 @@ typedef struct {
     int causal, window;
 } attn_ctx;
 
+#define ATTN_ROW_CHUNK 64
+
 static void attn_task(void* vctx, int64_t task) {
     attn_ctx* c = (attn_ctx*)vctx;
+    int64_t nchunk = (c->Sq + ATTN_ROW_CHUNK - 1) / ATTN_ROW_CHUNK;
+    int64_t chunk = task % nchunk;
+    task /= nchunk;
     int64_t b = task / c->Hq, h = task % c->Hq;
     int64_t ratio = c->Hq / c->Hkv;
     int64_t kvh = h / ratio;
@@ -274,7 +279,8 @@ static void attn_task(void* vctx, int64_t task) {
     float* ob = c->out + (b * c->Hq + h) * c->Sq * c->D;
     double* pr = (double*)malloc(sizeof(double) * (size_t)(c->Sk > 0 ? c->Sk : 1));
     double* acc = (double*)malloc(sizeof(double) * (size_t)c->D);
-    for (int64_t i = 0; i < c->Sq; i++) {
+    int64_t i_end = (chunk + 1) * ATTN_ROW_CHUNK < c->Sq ? (chunk + 1) * ATTN_ROW_CHUNK : c->Sq;
+    for (int64_t i = chunk * ATTN_ROW_CHUNK; i < i_end; i++) {
         double mx = -INFINITY;
         int64_t cnt = 0;
         for (int64_t j = 0; j < c->Sk; j++) {
@@ -339,7 +345,7 @@ ORACLE_API int32_t oracle_attention(const float* q, const float* k, const float*
         return rc;
     }
     attn_ctx c = {q, k, v, out, lse, B, Hq, Hkv, Sq, Sk, D, scale, causal != 0, window};
-    run_tasks(attn_task, &c, B * Hq, nthreads);
+    run_tasks(attn_task, &c, B * Hq * ((Sq + ATTN_ROW_CHUNK - 1) / ATTN_ROW_CHUNK), nthreads);
     return 0;
 }
 

@@ -1,0 +1,349 @@
+"""rdnattention_amd -- FlashAttention-2 forward for MI355X (gfx950), drop-in
+for the ``rdnattention`` Python package of dmonkman/RDNAttention.
+
+The public surface is the reference's (rdnattention/__init__.py:360-363):
+``flash_attn``, ``flash_attn_int8qk``, ``flash_attn_int8qk_quantized``,
+``quantize_int8_perchannel_v``, ``quantize_int8_qk_pertoken``,
+``has_device``, ``RDNAttentionError``, ``SUPPORTED_HEAD_DIMS``,
+``SUPPORTED_HEAD_DIMS_INT8`` and ``__version__``, with the same argument
+checks and exception types.  Every call goes through ``librdnattention.so``
+(HIP kernels for gfx950) on torch's current stream; there is no CPU
+fallback: a missing library raises ``RDNAttentionError``.
+
+    >>> import torch
+    >>> from rdnattention_amd import flash_attn
+    >>> q = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
+    >>> k = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
+    >>> v = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
+    >>> out = flash_attn(q, k, v, is_causal=True)
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+import platform
+from pathlib import Path
+
+logger = logging.getLogger(__name__)
+
+__version__ = "0.1.0"
+
+_lib = None
+
+SUPPORTED_HEAD_DIMS = tuple(range(32, 513, 32))
+SUPPORTED_HEAD_DIMS_INT8 = (64, 128)
+
+PATH_AUTO = 0
+PATH_PREFILL = 1
+PATH_SPLITK = 2
+
+
+class RDNAttentionError(Exception):
+    """Raised for any rdnattention library error."""
+
+
+def _find_library() -> Path:
+    """RDNATTENTION_LIB, else the in-tree build (rdnattention/__init__.py:37-73)."""
+    if platform.system() != "Linux":
+        raise RDNAttentionError(f"Unsupported platform: {platform.system()} (this build targets Linux/ROCm)")
+    override = os.environ.get("RDNATTENTION_LIB")
+    if override:
+        path = Path(override)
+        if not path.exists():
+            raise RDNAttentionError(f"RDNATTENTION_LIB points at a missing file: {path}")
+        logger.debug("Loading library from RDNATTENTION_LIB=%s", path)
+        return path
+    path = Path(__file__).resolve().parent / "lib" / "librdnattention.so"
+    if path.exists():
+        return path
+    raise RDNAttentionError(
+        f"Could not find the rdnattention library ({path}). Build it first: "
+        "python -m rdnattention_amd._build")
+
+
+_VP = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_U32 = ctypes.c_uint32
+_I32 = ctypes.c_int32
+_F32 = ctypes.c_float
+
+_FWD_ARGS = [_VP] * 6 + [_I64] * 12 + [_U32] * 6 + [_F32, _I32, _I32, _I32]
+_I8_ARGS = [_VP] * 4 + [_I64] * 12 + [_U32] * 6 + [_F32] * 4 + [_VP, _VP, _I32, _I32, _VP]
+
+
+def _lib_handle():
+    global _lib
+    if _lib is None:
+        lib = ctypes.CDLL(str(_find_library()))
+        lib.rdna_has_device.argtypes = []
+        lib.rdna_has_device.restype = _I32
+        lib.rdna_get_error.argtypes = []
+        lib.rdna_get_error.restype = ctypes.c_char_p
+        lib.rdna_attention_forward.argtypes = _FWD_ARGS + [_VP]
+        lib.rdna_attention_forward.restype = _I32
+        lib.rdna_attention_forward_path.argtypes = _FWD_ARGS + [_I32, _VP]
+        lib.rdna_attention_forward_path.restype = _I32
+        lib.rdna_attention_forward_int8qk.argtypes = _I8_ARGS
+        lib.rdna_attention_forward_int8qk.restype = _I32
+        lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
+        lib.rdna_int8_qk_scores.restype = _I32
+        lib.rdna_version.argtypes = []
+        lib.rdna_version.restype = ctypes.c_char_p
+        _lib = lib
+    return _lib
+
+
+def library_path() -> Path:
+    return Path(_lib_handle()._name)
+
+
+def has_device() -> bool:
+    """Whether a usable HIP device is present."""
+    return _lib_handle().rdna_has_device() == 1
+
+
+def last_error() -> str:
+    return _lib_handle().rdna_get_error().decode()
+
+
+def _validate_inputs(query, key, value, expected_dtype) -> None:
+    # rdnattention/__init__.py:138-155
+    import torch
+
+    if not isinstance(query, torch.Tensor):
+        raise TypeError("requires torch.Tensor inputs (GPU tensors already on this device)")
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError("requires torch.Tensor inputs (GPU tensors already on this device)")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a HIP device")
+        if t.dtype != expected_dtype:
+            raise ValueError(f"{name} must be {expected_dtype}, got {t.dtype}")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4D [batch, heads, seq, head_dim], got shape {tuple(t.shape)}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous - call .contiguous() first")
+    if query.shape[0] != key.shape[0] or query.shape[0] != value.shape[0]:
+        raise ValueError(f"Batch size must match: Q={query.shape}, K={key.shape}, V={value.shape}")
+    if key.shape[1] == 0 or query.shape[1] % key.shape[1] != 0:
+        raise ValueError(f"Q heads ({query.shape[1]}) must be a multiple of K heads ({key.shape[1]})")
+
+
+def _check_head_dim(head_dim: int, who: str, allowed=SUPPORTED_HEAD_DIMS):
+    # rdnattention/__init__.py:158-162
+    if head_dim not in allowed:
+        raise RDNAttentionError(
+            f"{who}: head_dim {head_dim} not supported "
+            f"(multiples of 32 from {allowed[0]} to {allowed[-1]})")
+
+
+def _rope_ptrs(rot_cos, rot_sin, query, seq_len, key_seq_len, head_dim):
+    """Validates the angle tables (rdnattention/__init__.py:165-192).
+    Returns (cos_ptr, sin_ptr, has_rope)."""
+    import torch
+
+    if rot_cos is None and rot_sin is None:
+        return None, None, 0
+    if rot_cos is None or rot_sin is None:
+        raise ValueError("pass both rot_cos and rot_sin, or neither")
+    rows = max(seq_len, key_seq_len)
+    for name, t in (("rot_cos", rot_cos), ("rot_sin", rot_sin)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.device != query.device:
+            raise ValueError(f"{name} must be on the same device as query")
+        if t.dtype != torch.float32:
+            raise ValueError(f"{name} must be float32, got {t.dtype}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous - call .contiguous() first")
+        if t.dim() != 2:
+            raise ValueError(f"{name} must be 2D [positions, head_dim // 2], got {tuple(t.shape)}")
+        if t.shape[1] != head_dim // 2:
+            raise ValueError(f"{name} must have head_dim // 2 = {head_dim // 2} columns, got {t.shape[1]}")
+        if t.shape[0] < rows:
+            raise ValueError(f"{name} needs at least max(seq_len, key_seq_len) = {rows} rows, got {t.shape[0]}")
+    return rot_cos.data_ptr(), rot_sin.data_ptr(), 1
+
+
+def _stream():
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def flash_attn(query, key, value, is_causal: bool = False, window_size: int = -1, rot_cos=None, rot_sin=None):
+    """FlashAttention-2 forward in fp16 (rdnattention/__init__.py:195-238).
+
+    query/key/value: contiguous float16 [batch, heads, seq, head_dim] on a HIP
+    device, head_dim in SUPPORTED_HEAD_DIMS; key/value may have fewer heads
+    (GQA/MQA, an exact divisor) and a different sequence length (decode,
+    cross-attention; causal aligns to the end of the keys).  rot_cos/rot_sin:
+    float32 [max(seq_len, key_seq_len), head_dim // 2] RoPE tables applied to
+    Q and K inside the kernel (channels 2i, 2i+1 rotate by column i).
+    The softmax scale is 1/sqrt(head_dim).  Returns a new tensor like query.
+    """
+    import torch
+
+    _validate_inputs(query, key, value, torch.float16)
+    _check_head_dim(query.shape[-1], "flash_attn")
+    if not has_device():
+        raise RDNAttentionError("no usable HIP device found")
+    batch, heads, seq_len, head_dim = query.shape
+    _, kv_heads, key_seq_len, _ = key.shape
+    cos_ptr, sin_ptr, has_rope = _rope_ptrs(rot_cos, rot_sin, query, seq_len, key_seq_len, head_dim)
+    output = torch.empty_like(query)
+    if output.numel() == 0:
+        return output
+    qs, ks, vs, os_ = query.stride(), key.stride(), value.stride(), output.stride()
+    result = _lib_handle().rdna_attention_forward(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(), cos_ptr, sin_ptr,
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
+        batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
+        head_dim ** -0.5, 1 if is_causal else 0, has_rope, window_size, _stream())
+    if result != 0:
+        raise RDNAttentionError(f"flash_attn failed: {last_error()}")
+    return output
+
+
+def attention_forward_into(query, key, value, output, *, is_causal: bool = False, window_size: int = -1,
+                           rot_cos=None, rot_sin=None, scale=None, path: int = PATH_AUTO) -> None:
+    """FP16 forward written into `output`, for strided tensors and explicit
+    kernel paths -- the direct C-ABI call the reference's own tools make
+    through ctypes (tests/rope.py:9-27, tests/benchmark.py:232-263).
+
+    query/key/value/output: float16 [batch, heads, seq, head_dim] views whose
+    head_dim axis is contiguous (any batch/head/seq strides that are multiples
+    of 8 elements, e.g. K/V sliced from a [B, S, 2, Hkv, D] cache).
+    `scale` defaults to 1/sqrt(head_dim); `path` is PATH_AUTO, PATH_PREFILL or
+    PATH_SPLITK.  Asynchronous on torch's current stream."""
+    import torch
+
+    for name, t in (("query", query), ("key", key), ("value", value), ("output", output)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.dtype != torch.float16 or t.dim() != 4 or not t.is_cuda:
+            raise ValueError(f"{name} must be a 4D float16 HIP tensor")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must have a contiguous head_dim axis")
+    if output.shape != query.shape:
+        raise ValueError("output must have the shape of query")
+    batch, heads, seq_len, head_dim = query.shape
+    _, kv_heads, key_seq_len, _ = key.shape
+    cos_ptr, sin_ptr, has_rope = _rope_ptrs(rot_cos, rot_sin, query, seq_len, key_seq_len, head_dim)
+    qs, ks, vs, os_ = query.stride(), key.stride(), value.stride(), output.stride()
+    result = _lib_handle().rdna_attention_forward_path(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(), cos_ptr, sin_ptr,
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
+        batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
+        float(head_dim ** -0.5 if scale is None else scale), 1 if is_causal else 0, has_rope, int(window_size),
+        int(path), _stream())
+    if result != 0:
+        raise RDNAttentionError(f"attention_forward_into failed: {last_error()}")
+
+
+def flash_attn_int8qk(query, key, value, q_scale, k_scale, v_scale: float, is_causal: bool = False,
+                      window_size: int = -1):
+    """INT8 attention, both GEMMs (rdnattention/__init__.py:241-300).
+
+    query/key/value: contiguous int8 [batch, heads, seq, head_dim], head_dim
+    in SUPPORTED_HEAD_DIMS_INT8.  q_scale/k_scale: float, or float32 tensors
+    of per-token scales shaped (batch, heads, seq_len) / (batch, kv_heads,
+    key_seq_len); v_scale: float.  Output float16.  No RoPE.
+    """
+    import torch
+
+    _validate_inputs(query, key, value, torch.int8)
+    heads, kv_heads_ = query.shape[1], key.shape[1]
+    if kv_heads_ == 0 or heads % kv_heads_ != 0:
+        raise RDNAttentionError(
+            f"flash_attn_int8qk: query heads ({heads}) must be a positive multiple of key/value heads ({kv_heads_})")
+    _check_head_dim(query.shape[-1], "flash_attn_int8qk", allowed=SUPPORTED_HEAD_DIMS_INT8)
+    if not has_device():
+        raise RDNAttentionError("no usable HIP device found")
+    batch, heads, seq_len, head_dim = query.shape
+    _, kv_heads, key_seq_len, _ = key.shape
+
+    def _scale_arg(x, name, want):
+        if not isinstance(x, torch.Tensor):
+            return float(x), None
+        t = x.to(dtype=torch.float32, device=query.device).contiguous()
+        if tuple(t.shape) != want:
+            raise RDNAttentionError(f"flash_attn_int8qk: {name} tensor must be {want}, got {tuple(t.shape)}")
+        return 1.0, t
+
+    q_scalar, q_vec = _scale_arg(q_scale, "q_scale", (batch, heads, seq_len))
+    k_scalar, k_vec = _scale_arg(k_scale, "k_scale", (batch, kv_heads, key_seq_len))
+    output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
+    if output.numel() == 0:
+        return output
+    qs, ks, vs, os_ = query.stride(), key.stride(), value.stride(), output.stride()
+    result = _lib_handle().rdna_attention_forward_int8qk(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
+        batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
+        head_dim ** -0.5, q_scalar, k_scalar, float(v_scale),
+        q_vec.data_ptr() if q_vec is not None else None, k_vec.data_ptr() if k_vec is not None else None,
+        1 if is_causal else 0, window_size, _stream())
+    if result != 0:
+        raise RDNAttentionError(f"flash_attn_int8qk failed: {last_error()}")
+    return output
+
+
+def quantize_int8_perchannel_v(query, key, value):
+    """(qi, ki, vi, q_scale, k_scale, v_scale, v_channel) with per-tensor Q/K
+    scales and one V scale per (batch, kv head, channel); v_scale = 1.0
+    (rdnattention/__init__.py:303-324).  Attention is linear in V, so
+    multiplying the output by v_channel undoes the V scaling exactly."""
+    import torch
+
+    def per_tensor(x):
+        s = x.abs().max().item() / 127.0
+        s = s if s != 0.0 else 1.0
+        return torch.clamp(torch.round(x / s), -127, 127).to(torch.int8), s
+
+    qi, q_scale = per_tensor(query.float())
+    ki, k_scale = per_tensor(key.float())
+    v = value.float()
+    v_channel = v.abs().amax(dim=-2, keepdim=True) / 127.0
+    v_channel = torch.where(v_channel == 0, torch.ones_like(v_channel), v_channel)
+    vi = torch.clamp(torch.round(v / v_channel), -127, 127).to(torch.int8)
+    return qi, ki, vi, q_scale, k_scale, 1.0, v_channel.squeeze(-2)
+
+
+def quantize_int8_qk_pertoken(query, key):
+    """(qi, ki, q_scale, k_scale) with one fp32 scale per (batch, head, row)
+    (rdnattention/__init__.py:327-343)."""
+    import torch
+
+    def per_token(x):
+        x = x.float()
+        s = x.abs().amax(dim=-1, keepdim=True) / 127.0
+        s = torch.where(s == 0, torch.ones_like(s), s)
+        return torch.clamp(torch.round(x / s), -127, 127).to(torch.int8), s.squeeze(-1).contiguous()
+
+    qi, q_scale = per_token(query)
+    ki, k_scale = per_token(key)
+    return qi, ki, q_scale, k_scale
+
+
+def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, window_size: int = -1):
+    """INT8 attention from ordinary fp16/fp32 Q/K/V (rdnattention/__init__.py:346-357):
+    per-token Q/K scales in-kernel and an exact per-channel V rescale after it.
+
+    Differs from the reference in one respect: v_channel is indexed by the kv
+    head of each query head, so grouped-query inputs with 1 < kv_heads < heads
+    work (the reference's broadcast raises there)."""
+    _, _, vi, _, _, v_scale, v_channel = quantize_int8_perchannel_v(query, key, value)
+    qi, ki, q_scale, k_scale = quantize_int8_qk_pertoken(query, key)
+    out = flash_attn_int8qk(qi.contiguous(), ki.contiguous(), vi.contiguous(), q_scale, k_scale, v_scale,
+                            is_causal, window_size)
+    ratio = query.shape[1] // key.shape[1]
+    if ratio > 1:
+        v_channel = v_channel.repeat_interleave(ratio, dim=1)
+    return (out.float() * v_channel.unsqueeze(-2)).to(out.dtype)
+
+
+__all__ = ["flash_attn", "flash_attn_int8qk", "flash_attn_int8qk_quantized", "quantize_int8_perchannel_v",
+           "quantize_int8_qk_pertoken", "has_device", "RDNAttentionError", "SUPPORTED_HEAD_DIMS",
+           "SUPPORTED_HEAD_DIMS_INT8", "__version__"]

@@ -1,0 +1,145 @@
+// Shared device-side building blocks for the gfx950 (CDNA4) attention kernels.
+//
+// Everything here is written for 64-lane wavefronts and the CDNA4 matrix
+// cores.  The MFMA operand conventions the kernels rely on:
+//
+//   v_mfma_f32_32x32x16_f16   D[32x32] += A[32x16] * B[16x32]
+//     A: lane l holds 8 halves of row m = l%32, reduction slots of group g = l/32
+//     B: lane l holds 8 halves of column n = l%32, the same reduction slots
+//     D: lane l holds D[8*(i/4) + 4*g + (i%4)][l%32], i = 0..15
+//
+// Only the D layout is load-bearing.  The reduction-slot order inside an
+// A/B register is the same for A and B, so any consistent assignment of the
+// reduction index to (g, element) gives the same dot product; the kernels
+// pick the one that makes every operand a single 16-byte LDS read.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rdna_amd {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+typedef int i16x __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f16x mfma_32x32x16_f16(h8 a, h8 b, f16x c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i16x mfma_32x32x32_i8(i4 a, i4 b, i16x c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+    // v_exp_f32: 2^x; exp2(-inf) = 0.
+    return __builtin_amdgcn_exp2f(x);
+}
+
+// Value of the lane whose index differs in bit 5 (the other half-wave).
+__device__ __forceinline__ float swap_halves(float x) {
+    return __shfl_xor(x, 32, 64);
+}
+
+__device__ __forceinline__ bool wave_any(bool pred) {
+    return __builtin_amdgcn_ballot_w64(pred) != 0;
+}
+
+// Masking rule of the reference (src/rdna/fa2_forward_f16.hip:325-348 and
+// docs/api.md:150-165), with delta = Sk - Sq:
+//   causal:             key <= q + delta
+//   causal + window w:  q + delta - key < w
+//   window w (no causal): |q + delta - key| <= w / 2
+//   always:             key < Sk
+struct MaskSpec {
+    int32_t sk;
+    int32_t delta;
+    int32_t causal;
+    int32_t window; // > 0 enables; 0 = off
+};
+
+__device__ __forceinline__ bool key_visible(const MaskSpec& m, int q, int key) {
+    bool ok = key < m.sk;
+    int rel = q + m.delta - key;
+    if (m.causal) {
+        ok = ok && rel >= 0;
+    }
+    if (m.window > 0) {
+        if (m.causal) {
+            ok = ok && rel < m.window;
+        } else {
+            int a = rel < 0 ? -rel : rel;
+            ok = ok && a <= (m.window >> 1);
+        }
+    }
+    return ok;
+}
+
+// Inclusive key interval [lo, hi] any row in [q_lo, q_hi] can see.
+// Empty when hi < lo.
+__device__ __forceinline__ void visible_key_range(const MaskSpec& m, int q_lo, int q_hi, int& lo, int& hi) {
+    lo = 0;
+    hi = m.sk - 1;
+    if (m.causal) {
+        hi = min(hi, q_hi + m.delta);
+    }
+    if (m.window > 0) {
+        if (m.causal) {
+            lo = max(lo, q_lo + m.delta - m.window + 1);
+        } else {
+            int hw = m.window >> 1;
+            lo = max(lo, q_lo + m.delta - hw);
+            hi = min(hi, q_hi + m.delta + hw);
+        }
+    }
+}
+
+// Classify a key tile [k_lo, k_hi] against rows [q_lo, q_hi]:
+//   0 = no key visible to any row (skip), 1 = every pair visible (no mask),
+//   2 = mixed (apply the per-element mask).
+__device__ __forceinline__ int classify_tile(const MaskSpec& m, int q_lo, int q_hi, int k_lo, int k_hi) {
+    int lo, hi;
+    visible_key_range(m, q_lo, q_hi, lo, hi);
+    if (hi < lo || k_hi < lo || k_lo > hi) {
+        return 0;
+    }
+    bool full = k_hi < m.sk;
+    if (m.causal) {
+        full = full && (k_hi <= q_lo + m.delta);
+    }
+    if (m.window > 0) {
+        if (m.causal) {
+            full = full && (k_lo > q_hi + m.delta - m.window);
+        } else {
+            int hw = m.window >> 1;
+            full = full && (k_lo >= q_hi + m.delta - hw) && (k_hi <= q_lo + m.delta + hw);
+        }
+    }
+    return full ? 1 : 2;
+}
+
+// RoPE on 8 consecutive channels (4 interleaved pairs) of one row:
+// (a, b) -> (a*c - b*s, a*s + b*c) in fp32, rounded to fp16, where c/s are
+// table columns col0 .. col0+3 (src/rdna/fa2_forward_f16.hip:63-77).
+__device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin_row, int col0) {
+    f4 c = *reinterpret_cast<const f4*>(cos_row + col0);
+    f4 s = *reinterpret_cast<const f4*>(sin_row + col0);
+    h8 y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = (float)x[2 * i];
+        float b = (float)x[2 * i + 1];
+        y[2 * i] = (_Float16)(a * c[i] - b * s[i]);
+        y[2 * i + 1] = (_Float16)(a * s[i] + b * c[i]);
+    }
+    return y;
+}
+
+} // namespace rdna_amd

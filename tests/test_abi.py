@@ -1,0 +1,186 @@
+"""CPU-side checks of the C ABI boundary (no GPU needed):
+
+* librdnattention.so loads and exports every symbol declared in include/*.h
+  (the four drop-in symbols of the reference's src/c_api.hpp:16-87 plus the
+  extensions in rdnattention_ext.h) and the reference's C++ launch API;
+* every argument check runs before any HIP call and reports -3 with the
+  reference's message format ("Attention (fp16) failed: ...");
+* the Python wrapper raises the reference's exception types for bad input.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+LIB = ROOT / "rdnattention_amd" / "lib" / "librdnattention.so"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        from rdnattention_amd import _build
+
+        _build.build()
+    import rdnattention_amd
+
+    return rdnattention_amd._lib_handle()
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        names.update(re.findall(r"RDNA_API\s+[\w\s\*]+?\b(rdna_\w+)\s*\(", text))
+    return names
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = _declared_symbols()
+    assert {"rdna_has_device", "rdna_get_error", "rdna_attention_forward",
+            "rdna_attention_forward_int8qk"} <= declared
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s+(\S+)", out))
+    missing = declared - exported
+    assert not missing, f"declared but not exported: {missing}"
+    # the reference's C++ API (src/rdna/fa2_forward_f16.hpp, fa2_forward_int8qk.hpp)
+    for mangled in ("_ZN4rdna10forwardF16ERKNS_13ForwardParamsEPv", "_ZN4rdna9lastErrorEv", "_ZN4rdna9hasDeviceEv",
+                    "_ZN4rdna13forwardInt8QKERKNS_19ForwardParamsInt8QKEPv", "_ZN4rdna15lastErrorInt8QKEv"):
+        assert mangled in exported
+
+
+def test_version(lib):
+    assert lib.rdna_version().decode().startswith("0.1.0")
+
+
+def _buf(n=4096):
+    # 16-byte aligned host buffer; never dereferenced by the rejected calls below
+    a = np.zeros(n + 16, dtype=np.uint8)
+    off = (-a.ctypes.data) % 16
+    return a, a.ctypes.data + off
+
+
+def _fwd(lib, **kw):
+    hold, p = _buf()
+    args = dict(q=p, k=p, v=p, o=p, cos=None, sin=None, strides=(64 * 8 * 64, 8 * 64, 64), B=1, Hq=8, Hkv=8, Sq=8,
+                Sk=8, D=64, scale=0.125, causal=0, rope=0, window=-1)
+    args.update(kw)
+    s = args["strides"]
+    rc = lib.rdna_attention_forward(args["q"], args["k"], args["v"], args["o"], args["cos"], args["sin"],
+                                    *s, *s, *s, *s, args["B"], args["Hq"], args["Hkv"], args["Sq"], args["Sk"],
+                                    args["D"], args["scale"], args["causal"], args["rope"], args["window"], None)
+    return rc, lib.rdna_get_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=48), "unsupported head_dim (multiples of 32 from 32 to 512)"),
+    (dict(D=544), "unsupported head_dim"),
+    (dict(D=0), "unsupported head_dim"),
+    (dict(Hkv=3), "numHeads must be a positive multiple of numKvHeads"),
+    (dict(Hkv=0), "numHeads must be a positive multiple of numKvHeads"),
+    (dict(Sq=0), "empty launch grid"),
+    (dict(B=0), "empty launch grid"),
+    (dict(q=None), "null tensor pointer"),
+    (dict(strides=(4096, 512, 68)), "multiples of 16 bytes"),
+    (dict(rope=1), "rot_cos/rot_sin is null"),
+    (dict(Sq=(1 << 30) + 1), "exceed the supported range"),
+])
+def test_fp16_argument_errors(lib, kw, msg):
+    rc, err = _fwd(lib, **kw)
+    assert rc == -3
+    assert err.startswith("Attention (fp16) failed: ")
+    assert msg in err
+
+
+def test_misaligned_pointer_rejected(lib):
+    hold, p = _buf()
+    rc, err = _fwd(lib, q=p + 2)
+    assert rc == -3 and "16-byte aligned" in err
+
+
+def test_error_is_thread_local_and_sticky(lib):
+    import threading
+
+    _fwd(lib, D=48)
+    seen = {}
+
+    def other():
+        seen["err"] = lib.rdna_get_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["err"] == ""  # a fresh thread has no error
+    assert "head_dim" in lib.rdna_get_error().decode()  # not cleared
+
+
+def _i8(lib, **kw):
+    hold, p = _buf()
+    args = dict(B=1, Hq=8, Hkv=8, Sq=8, Sk=8, D=64, strides=(8 * 8 * 64, 8 * 64, 64))
+    args.update(kw)
+    s = args["strides"]
+    rc = lib.rdna_attention_forward_int8qk(p, p, p, p, *s, *s, *s, *s, args["B"], args["Hq"], args["Hkv"],
+                                           args["Sq"], args["Sk"], args["D"], 0.125, 1.0, 1.0, 1.0, None, None, 0,
+                                           -1, None)
+    return rc, lib.rdna_get_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=96), "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)"),
+    (dict(Hkv=0), "numHeads must be a positive multiple of numKvHeads"),
+    (dict(Hkv=3, D=96), "numHeads must be a positive multiple of numKvHeads"),  # ratio checked first
+    (dict(strides=(4096, 512, 72)), "multiples of 16 bytes"),
+])
+def test_int8_argument_errors(lib, kw, msg):
+    rc, err = _i8(lib, **kw)
+    assert rc == -3
+    assert err.startswith("Attention (int8qk) failed: ")
+    assert msg in err
+
+
+def test_has_device_without_gpu(lib):
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("GPU host")
+    assert lib.rdna_has_device() == 0
+
+
+# --------------------------------------------------------------------------- #
+# Python wrapper argument checks (rdnattention/__init__.py:138-192)
+# --------------------------------------------------------------------------- #
+def test_python_type_errors():
+    import torch
+
+    import rdnattention_amd as ra
+
+    with pytest.raises(TypeError):
+        ra.flash_attn(np.zeros((1, 1, 1, 64)), None, None)
+    cpu = torch.zeros(1, 2, 4, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="must be on a HIP device"):
+        ra.flash_attn(cpu, cpu, cpu)
+
+
+def test_python_head_dim_lists():
+    import rdnattention_amd as ra
+
+    assert ra.SUPPORTED_HEAD_DIMS == tuple(range(32, 513, 32))
+    assert ra.SUPPORTED_HEAD_DIMS_INT8 == (64, 128)
+    with pytest.raises(ra.RDNAttentionError, match="head_dim 48 not supported"):
+        ra._check_head_dim(48, "flash_attn")
+    assert set(ra.__all__) == {"flash_attn", "flash_attn_int8qk", "flash_attn_int8qk_quantized",
+                               "quantize_int8_perchannel_v", "quantize_int8_qk_pertoken", "has_device",
+                               "RDNAttentionError", "SUPPORTED_HEAD_DIMS", "SUPPORTED_HEAD_DIMS_INT8",
+                               "__version__"}
+
+
+def test_python_missing_library(monkeypatch, tmp_path):
+    import rdnattention_amd as ra
+
+    monkeypatch.setenv("RDNATTENTION_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(ra, "_lib", None)
+    with pytest.raises(ra.RDNAttentionError, match="missing file"):
+        ra.has_device()

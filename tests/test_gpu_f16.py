@@ -1,0 +1,251 @@
+"""FP16 parity on the GPU: librdnattention.so (through the C ABI and the
+Python wrapper) against the CPU oracle on the same inputs.
+
+Case lists restate the reference's own suites:
+  * GATE_CASES   -- tests/hip_forward_gate.hip:259-316 (50 cases, LCG seed 12345)
+  * HEAD_DIM_VARIANTS -- tests/head_dim.py:10-20 (9 variants x 16 head dims, seed 1234)
+  * ROPE_CASES   -- tests/rope.py:66-73 (7 cases, seed 7)
+Bars: max-abs <= 2e-3, mean-abs <= 2e-4 and the gate's rel_rms < 5e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.gpu_util import (assert_f16_parity, forward_raw, gate_rope_tables, lcg_inputs, log, reference_f16,
+                            seeded_inputs)
+
+pytestmark = pytest.mark.gpu
+
+LARGE_D_PENDING = 256  # head dims above this use the large-head kernel
+
+# name, batch, numHeads, numKvHeads, seqLen, keySeqLen, headDim, causal, windowSize, hasRope
+GATE_CASES = [
+    ("d64_dense_small", 1, 4, 4, 96, 96, 64, False, 0, False),
+    ("d64_dense_tail", 2, 4, 4, 200, 200, 64, False, 0, False),
+    ("d64_causal", 1, 4, 4, 257, 257, 64, True, 0, False),
+    ("d64_gqa_causal", 1, 8, 2, 300, 300, 64, True, 0, False),
+    ("d64_gqa_ratio2_exact", 1, 8, 4, 300, 300, 64, True, 0, False),
+    ("d64_gqa_ratio8", 1, 16, 2, 300, 300, 64, True, 0, False),
+    ("d64_gqa_ratio3_pad", 2, 6, 2, 257, 257, 64, True, 0, False),
+    ("d64_gqa_ratio6_even", 1, 12, 2, 300, 300, 64, False, 0, False),
+    ("d64_gqa_ratio5_pad", 2, 10, 2, 199, 199, 64, True, 64, True),
+    ("d64_gqa_batch4", 4, 8, 2, 96, 96, 64, False, 0, False),
+    ("d64_mqa", 2, 8, 1, 199, 199, 64, True, 0, False),
+    ("d64_gqa_decode_1tok", 1, 8, 2, 1, 300, 64, False, 0, False),
+    ("d64_gqa_decode_few", 2, 16, 4, 4, 300, 64, False, 0, False),
+    ("d64_gqa_window", 1, 8, 2, 300, 300, 64, False, 64, False),
+    ("d64_gqa_numkv8", 1, 32, 8, 256, 256, 64, True, 0, True),
+    ("d64_window", 1, 4, 4, 300, 300, 64, False, 64, False),
+    ("d64_causal_window", 1, 4, 4, 300, 300, 64, True, 32, False),
+    ("d64_rope_causal", 2, 4, 4, 271, 271, 64, True, 0, True),
+    ("d64_kv_longer", 1, 4, 4, 64, 300, 64, False, 0, False),
+    ("d128_dense", 1, 4, 4, 130, 130, 128, False, 0, False),
+    ("d128_causal", 1, 4, 4, 150, 150, 128, True, 0, False),
+    ("d128_rope_gqa_causal", 1, 8, 4, 199, 199, 128, True, 0, True),
+    ("d32_dense", 1, 2, 2, 100, 100, 32, False, 0, False),
+    ("d96_dense", 1, 2, 2, 100, 100, 96, False, 0, False),
+    ("d160_dense", 1, 2, 2, 100, 100, 160, False, 0, False),
+    ("d192_dense", 1, 2, 2, 100, 100, 192, False, 0, False),
+    ("d224_dense", 1, 2, 2, 100, 100, 224, False, 0, False),
+    ("d256_dense", 1, 2, 2, 100, 100, 256, False, 0, False),
+    ("d288_dense", 1, 2, 2, 100, 100, 288, False, 0, False),
+    ("d320_dense", 1, 2, 2, 100, 100, 320, False, 0, False),
+    ("d352_dense", 1, 2, 2, 100, 100, 352, False, 0, False),
+    ("d384_dense", 1, 2, 2, 100, 100, 384, False, 0, False),
+    ("d416_dense", 1, 2, 2, 100, 100, 416, False, 0, False),
+    ("d448_dense", 1, 2, 2, 100, 100, 448, False, 0, False),
+    ("d480_dense", 1, 2, 2, 100, 100, 480, False, 0, False),
+    ("d512_dense", 1, 2, 2, 100, 100, 512, False, 0, False),
+    ("d384_causal", 1, 2, 2, 100, 100, 384, True, 0, False),
+    ("d384_gqa_causal", 1, 8, 2, 100, 100, 384, True, 0, False),
+    ("d384_window", 1, 2, 2, 100, 100, 384, False, 32, False),
+    ("d384_causal_window", 1, 2, 2, 100, 100, 384, True, 32, False),
+    ("d384_rope_causal", 1, 2, 2, 100, 100, 384, True, 0, True),
+    ("d384_kv_longer", 1, 2, 2, 40, 100, 384, False, 0, False),
+    ("d384_decode_1tok", 1, 4, 2, 1, 100, 384, False, 0, False),
+    ("d512_causal", 1, 2, 2, 100, 100, 512, True, 0, False),
+    ("d512_gqa_rope_causal", 1, 4, 2, 100, 100, 512, True, 0, True),
+    ("d512_window", 1, 2, 2, 100, 100, 512, False, 32, False),
+    ("d512_kv_longer", 1, 2, 2, 40, 100, 512, False, 0, False),
+    ("d256_rope_causal", 1, 2, 2, 100, 100, 256, True, 0, True),
+    ("d256_gqa_window", 1, 8, 2, 100, 100, 256, False, 32, False),
+    ("d352_causal_aligned", 1, 2, 2, 96, 96, 352, True, 0, False),
+]
+
+
+def _skip_large(d):
+    if d > LARGE_D_PENDING:
+        pytest.skip("head_dim > 256: large-head kernel not built yet")
+
+
+@pytest.mark.parametrize("case", GATE_CASES, ids=[c[0] for c in GATE_CASES])
+def test_gate_cases(gpu, oracle_lib, case):
+    name, b, hq, hkv, sq, sk, d, causal, window, rope = case
+    _skip_large(d)
+    log(f"[gate] {name}")
+    q, k, v = lcg_inputs(12345, b, hq, hkv, sq, sk, d, mode=0)
+    cos = sin = None
+    if rope:
+        cos, sin = gate_rope_tables(max(sq, sk), d)
+    ref = reference_f16(q, k, v, causal, window, cos, sin)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    out = torch.empty_like(qd)
+    rc = forward_raw(qd, kd, vd, out, causal, window,
+                     torch.from_numpy(cos).to(gpu) if rope else None,
+                     torch.from_numpy(sin).to(gpu) if rope else None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_f16_parity(out.float().cpu().numpy(), ref, name)
+
+
+HEAD_DIM_VARIANTS = [
+    ("dense", 1, 300, 300, False, -1),
+    ("causal", 1, 300, 300, True, -1),
+    ("gqa", 4, 300, 300, False, -1),
+    ("gqa_causal", 4, 300, 300, True, -1),
+    ("window", 1, 300, 300, False, 64),
+    ("causal_window", 1, 300, 300, True, 32),
+    ("cross", 1, 200, 300, False, -1),
+    ("decode", 1, 1, 300, False, -1),
+    ("aligned", 1, 256, 256, True, -1),
+]
+
+
+@pytest.mark.parametrize("d", list(range(32, 513, 32)))
+@pytest.mark.parametrize("variant", HEAD_DIM_VARIANTS, ids=[v[0] for v in HEAD_DIM_VARIANTS])
+def test_head_dim_python_path(gpu, oracle_lib, d, variant):
+    """tests/head_dim.py through rdnattention_amd.flash_attn (8 heads, N(0,1))."""
+    import rdnattention_amd
+
+    _skip_large(d)
+    name, kvdiv, s_len, ks_len, causal, window = variant
+    torch.manual_seed(1234)
+    h = 8
+    kvh = max(1, h // kvdiv)
+    q = torch.randn(1, h, s_len, d, dtype=torch.float16)
+    k = torch.randn(1, kvh, ks_len, d, dtype=torch.float16)
+    v = torch.randn(1, kvh, ks_len, d, dtype=torch.float16)
+    out = rdnattention_amd.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal, window_size=window)
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, causal, window)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_{name}")
+
+
+ROPE_CASES = [
+    ("MHA d64 rope", 1, 8, 8, 256, 256, 64, False),
+    ("MHA d128 rope", 2, 8, 8, 512, 512, 128, False),
+    ("causal d64 rope", 1, 8, 8, 256, 256, 64, True),
+    ("causal d128 rope", 1, 8, 8, 384, 384, 128, True),
+    ("GQA d64 rope", 1, 8, 2, 256, 256, 64, False),
+    ("cross-attn d64 rope", 1, 8, 8, 128, 512, 64, False),
+    ("tail 300 rope", 1, 8, 8, 300, 300, 64, False),
+]
+
+
+@pytest.mark.parametrize("case", ROPE_CASES, ids=[c[0] for c in ROPE_CASES])
+def test_rope_cases(gpu, oracle_lib, case):
+    """tests/rope.py:66-96 through rdnattention_amd.flash_attn with in-kernel RoPE."""
+    import rdnattention_amd
+
+    name, b, h, kh, s, ks, d, causal = case
+    torch.manual_seed(7)
+    q = torch.randn(b, h, s, d, dtype=torch.float16)
+    k = torch.randn(b, kh, ks, d, dtype=torch.float16)
+    v = torch.randn(b, kh, ks, d, dtype=torch.float16)
+    cos, sin = oracle.rope_tables(max(s, ks), d)
+    out = rdnattention_amd.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal,
+                                      rot_cos=torch.from_numpy(cos).to(gpu), rot_sin=torch.from_numpy(sin).to(gpu))
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, causal, -1, cos, sin)
+    assert_f16_parity(out.float().cpu().numpy(), ref, name)
+    # the reference's own bar against an un-rounded RoPE (tests/rope.py:92-95)
+    ref_fp32_rope = oracle.attention(oracle.rope(q.float().numpy(), cos, sin, round_f16=False),
+                                     oracle.rope(k.float().numpy(), cos, sin, round_f16=False), v.float().numpy(),
+                                     causal=causal)
+    got = out.float().cpu().numpy().astype(np.float64)
+    rel = np.sqrt(((got - ref_fp32_rope) ** 2).mean() / (ref_fp32_rope ** 2).mean())
+    assert rel < 1e-2
+
+
+def test_quick_start_shape(gpu, oracle_lib):
+    """B=1, H=8, S=512, D=64, non-causal, N(0,1) seed 0."""
+    q, k, v = seeded_inputs(0, 1, 8, 8, 512, 512, 64)
+    out = torch.empty_like(q, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out) == 0
+    torch.cuda.synchronize()
+    assert_f16_parity(out.float().cpu().numpy(), reference_f16(q, k, v, False, -1), "quick_start")
+
+
+def test_strided_kv_views_bit_identical(gpu, oracle_lib):
+    """K/V as head-strided views of one [B,S,2,Hkv,D] buffer: the result is
+    bit-identical to contiguous copies and matches the oracle."""
+    g = torch.Generator().manual_seed(3)
+    b, hq, hkv, sq, sk, d = 2, 8, 2, 37, 333, 128
+    buf = torch.randn(b, sk, 2, hkv, d, generator=g).half().to(gpu)
+    q = torch.randn(b, hq, sq, d, generator=g).half().to(gpu)
+    kv_k = buf[:, :, 0].transpose(1, 2)
+    kv_v = buf[:, :, 1].transpose(1, 2)
+    assert not kv_k.is_contiguous()
+    o1 = torch.empty_like(q)
+    o2 = torch.empty_like(q)
+    assert forward_raw(q, kv_k, kv_v, o1) == 0
+    assert forward_raw(q, kv_k.contiguous(), kv_v.contiguous(), o2) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    ref = reference_f16(q.cpu(), kv_k.cpu(), kv_v.cpu(), False, -1)
+    assert_f16_parity(o1.float().cpu().numpy(), ref, "strided")
+
+
+def test_strided_output_and_query(gpu, oracle_lib):
+    """Q and O as [B,S,H,D]-layout views (seq stride H*D)."""
+    g = torch.Generator().manual_seed(4)
+    b, h, s, d = 2, 4, 65, 64
+    qb = torch.randn(b, s, h, d, generator=g).half().to(gpu)
+    kb = torch.randn(b, s, h, d, generator=g).half().to(gpu)
+    vb = torch.randn(b, s, h, d, generator=g).half().to(gpu)
+    ob = torch.zeros(b, s, h, d, dtype=torch.float16, device=gpu)
+    q, k, v, o = (t.transpose(1, 2) for t in (qb, kb, vb, ob))
+    assert forward_raw(q, k, v, o, causal=True) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q.cpu(), k.cpu(), v.cpu(), True, -1)
+    assert_f16_parity(o.float().cpu().numpy(), ref, "strided_o")
+
+
+def test_rows_without_keys_are_zero(gpu, oracle_lib):
+    """Causal with Sq > Sk: the first Sq - Sk rows see no key and are written as 0."""
+    q, k, v = seeded_inputs(5, 1, 2, 2, 100, 40, 64)
+    out = torch.full_like(q, 7.0, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal=True) == 0
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    assert np.all(o[:, :, :60] == 0.0)
+    assert_f16_parity(o, reference_f16(q, k, v, True, -1), "no_keys")
+
+
+def test_first_causal_row_exact(gpu):
+    q, k, v = seeded_inputs(6, 1, 4, 4, 128, 128, 128)
+    out = torch.empty_like(q, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal=True) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :, 0].cpu(), v[:, :, 0])
+
+
+def test_negative_and_zero_scale(gpu, oracle_lib):
+    """`scale` is honoured as passed through the C ABI, including <= 0."""
+    q, k, v = seeded_inputs(8, 1, 2, 2, 70, 90, 64)
+    for scale in (-0.125, 0.0, 0.3):
+        out = torch.empty_like(q, device=gpu)
+        assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal=True, scale=scale) == 0
+        torch.cuda.synchronize()
+        ref = oracle.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=True, scale=scale)
+        assert_f16_parity(out.float().cpu().numpy(), ref, f"scale={scale}")
+
+
+def test_empty_key_sequence_outputs_zero(gpu):
+    q = torch.randn(1, 2, 10, 64, dtype=torch.float16, device=gpu)
+    k = torch.empty(1, 2, 0, 64, dtype=torch.float16, device=gpu)
+    out = torch.full_like(q, 3.0)
+    assert forward_raw(q, k, k, out) == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out) == 0
