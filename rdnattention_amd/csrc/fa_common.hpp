@@ -43,9 +43,32 @@ __device__ __forceinline__ float fast_exp2(float x) {
     return __builtin_amdgcn_exp2f(x);
 }
 
-// Value of the lane whose index differs in bit 5 (the other half-wave).
-__device__ __forceinline__ float swap_halves(float x) {
-    return __shfl_xor(x, 32, 64);
+// ds_read_b64_tr_b16 (gfx950 LDS transpose read).  Within each 16-lane
+// group, lane i receives as half k the half (i % 4) of the 8-byte word whose
+// address lane 4k + i/4 supplies.  So if lane j of the group points at
+// row (j / 4), columns 4 * (j % 4) .. +3 of a row-major 4 x 16 block, lane i
+// gets column i of the block: the four rows' values, i.e. a transposed read.
+typedef __fp16 fp16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+__device__ __forceinline__ h4 lds_read_tr16(const _Float16* p) {
+    typedef __attribute__((address_space(3))) fp16x4_raw lds_h4;
+    const auto* lp = reinterpret_cast<const __attribute__((address_space(3))) char*>(
+        (uint32_t)reinterpret_cast<uintptr_t>(p));
+    fp16x4_raw r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_h4*)lp);
+    return __builtin_bit_cast(h4, r);
+}
+
+// max(x[l], x[l ^ 32]): combine the two half-waves that hold the same query
+// column.  v_permlane32_swap exchanges lanes 0-31 of one operand with lanes
+// 32-63 of the other, so the pair {r[0], r[1]} is {x[l % 32], x[32 + l % 32]}
+// in every lane.
+__device__ __forceinline__ float pair_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ bool wave_any(bool pred) {
@@ -123,6 +146,36 @@ __device__ __forceinline__ int classify_tile(const MaskSpec& m, int q_lo, int q_
         }
     }
     return full ? 1 : 2;
+}
+
+// Visible keys of one query row q form the interval [lo, hi] (empty when
+// hi < lo).  Same rule as key_visible, evaluated once per row so that masking a
+// tile is two compares per score instead of a branchy predicate.
+__device__ __forceinline__ void row_key_bounds(const MaskSpec& m, int q, int& lo, int& hi) {
+    visible_key_range(m, q, q, lo, hi);
+}
+
+// Raw buffer resource (gfx9 V#: stride 0, DATA_FORMAT 32): loads at byte
+// offsets >= num_records return 0, which is how rows past the end of K/V read
+// as zeros without per-load branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_records) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
+}
+
+__device__ __forceinline__ h8 buffer_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    typedef unsigned u4 __attribute__((ext_vector_type(4)));
+    u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return __builtin_bit_cast(h8, x);
+}
+
+// Bytes of a strided row range [row0, n_rows) of a row-major tensor with
+// `row_bytes` per row and `stride_bytes` between rows, clamped to 32 bits.
+__device__ __forceinline__ uint32_t range_bytes(int64_t rows_left, int64_t stride_bytes, int64_t row_bytes) {
+    if (rows_left <= 0) {
+        return 0;
+    }
+    int64_t n = (rows_left - 1) * stride_bytes + row_bytes;
+    return n > 0xffffffffll ? 0xffffffffu : (uint32_t)n;
 }
 
 // RoPE on 8 consecutive channels (4 interleaved pairs) of one row:

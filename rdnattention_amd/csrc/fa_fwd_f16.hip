@@ -1,4 +1,5 @@
-// FP16 FlashAttention-2 forward for gfx950 (MI355X): prefill kernel.
+// FP16 FlashAttention-2 forward for gfx950 (MI355X): prefill kernel and the
+// FP16 dispatcher.
 //
 // Replaces the reference's forwardKernel / forwardKernelGqa
 // (src/rdna/fa2_forward_f16.hip:633-877) with a CDNA4 MFMA design:
@@ -13,14 +14,20 @@
 //   * V is transposed into LDS (sVT[d][key]) with the key quads of every
 //     16-key group stored in the order 0,2,1,3 -- the order P^T's rows come
 //     out of the accumulator -- so each A operand is one 16-byte LDS read
-//   * key tiles outside the causal/window band are skipped per workgroup,
-//     tiles fully inside it run without any per-element mask
-//   * K/V tiles for step t+1 are loaded from HBM into registers while step
-//     t computes; RoPE is applied to Q once and to K while staging it
+//   * LDS is double-buffered: tile t+1 is written while tile t is read, one
+//     barrier per tile; tile t+2 is in flight from HBM meanwhile
+//   * key tiles outside the causal/window band are skipped, tiles inside it
+//     run a mask-free path, only boundary tiles evaluate the mask
+//   * the running max is only raised when it grows by more than 2^8 (the
+//     result is the same softmax; P stays <= 256, exact in fp16's range), so
+//     the O accumulator is rarely rescaled
+//   * RoPE: Q is rotated once when loaded, K once up front (fa_rope.hip)
 #include "fa_common.hpp"
 #include "fa_host.hpp"
+#include "fa_internal.hpp"
 
 #include <algorithm>
+#include <cmath>
 
 namespace rdna_amd {
 namespace {
@@ -42,40 +49,130 @@ struct PrefillParams {
     int32_t n_row_tiles;   // ceil(Sq / rows_per_wg)
     int32_t n_head_groups; // B * Hkv * groups_per_kv
     int32_t groups_per_kv; // ratio / G
-    float c;               // |scale| * log2(e)
+    float c;               // max(|scale| * log2(e), 1e-30)
     float q_sign;          // sign of scale, folded into Q (exact in fp16)
     MaskSpec mask;
-    int32_t has_rope;
+    int32_t rope_q;        // rotate Q with rot_cos / rot_sin while loading it
 };
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBN = 64; // keys per tile
+constexpr int kBN = 64;                 // keys per tile
+constexpr float kRescaleThreshold = 8.0f; // log2 units
 
 template <int D>
 struct PrefillCfg {
-    static constexpr int K_LD = D + 8;     // sK row stride (halves); +16 B keeps b128 reads conflict-free
-    static constexpr int VT_LD = kBN + 8;  // sVT row stride (halves)
-    static constexpr int NS = D / 16;      // QK^T reduction steps
-    static constexpr int NDT = D / 32;     // O^T row tiles
-    static constexpr int KCH = D / 8;      // 16-byte chunks per K/V row
-    static constexpr int KTASK = kBN * KCH;
-    static constexpr int KT = (KTASK + kThreads - 1) / kThreads;
-    static constexpr int VTASK = (kBN / 4) * KCH; // (key quad, chunk) pairs
-    static constexpr int VT = (VTASK + kThreads - 1) / kThreads;
+    // K and V tiles are row-major [64 keys][D] in LDS with a 32-byte row pad:
+    // rows 0..7 then start in distinct 32-byte bank groups, which keeps both
+    // the ds_read_b128 of K and the 4-row ds_read_b64_tr_b16 of V conflict-free
+    static constexpr int LD = D + 16;
+    static constexpr int TILE_ELEMS = kBN * LD;
+    static constexpr int BUF_ELEMS = 2 * TILE_ELEMS; // K then V
+    static constexpr int NS = D / 16;                // QK^T reduction steps
+    static constexpr int NDT = D / 32;               // O^T row tiles
+    static constexpr int KCH = D / 8;                // 16-byte chunks per K/V row
+    static constexpr int TASK = kBN * KCH;
+    static constexpr int KT = (TASK + kThreads - 1) / kThreads;
     static constexpr int MIN_WG = D <= 128 ? 2 : 1;
 };
 
-// Position of the key quad `qd` (0..3) of a 16-key group inside sVT.
-__device__ __forceinline__ int vt_quad_pos(int qd) {
-    return qd == 1 ? 2 : (qd == 2 ? 1 : qd);
+// One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// `prefetch` (staging of the next tiles) is issued right behind the S^T
+// MFMAs so its LDS stores and HBM loads overlap them; the exponentials of the
+// second 32-key half overlap the PV MFMAs of the first.
+template <int D, bool MASKED, class Prefetch>
+__device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const _Float16* __restrict__ sV,
+                                          const h8 (&qreg)[PrefillCfg<D>::NS], f16x (&oacc)[PrefillCfg<D>::NDT],
+                                          float& m_run, float& l_run, int klo, int khi, int kt0, float c, int lane,
+                                          Prefetch&& prefetch) {
+    using C = PrefillCfg<D>;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    f16x sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+        f16x acc = {};
+#pragma unroll
+        for (int s = 0; s < C::NS; s++) {
+            h8 a = *reinterpret_cast<const h8*>(&sK[(kt * 32 + l32) * C::LD + 16 * s + 8 * g]);
+            acc = mfma_32x32x16_f16(a, qreg[s], acc);
+        }
+        sacc[kt] = acc;
+    }
+    prefetch();
+    if constexpr (MASKED) {
+        // visible iff klo <= key <= khi, key = kt0 + 4g + (compile-time offset)
+        const int a = klo - kt0 - 4 * g;
+        const int b = khi - kt0 - 4 * g;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int off = kt * 32 + 8 * (i >> 2) + (i & 3);
+                sacc[kt][i] = (off < a || off > b) ? -INFINITY : sacc[kt][i];
+            }
+        }
+    }
+    float mx = sacc[0][0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) {
+        mx = fmaxf(mx, sacc[0][i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        mx = fmaxf(mx, sacc[1][i]);
+    }
+    mx = pair_max(mx);
+    const float m_new = fmaxf(m_run, mx * c); // c > 0: -inf stays -inf
+    const bool grow = m_new > m_run + kRescaleThreshold;
+    if (wave_any(grow)) {
+        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
+        if (grow) {
+            m_run = m_new;
+        }
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; dt++) {
+            oacc[dt] *= alpha;
+        }
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+
+    // V^T operand rows via transpose reads: lane j of each 16-lane group points
+    // at key row 4g + j/4 (+8 for the second half of the slots), columns
+    // 16*(lane/16 % 2) + 4*(j % 4) of the 32-column d tile
+    const int j16 = lane & 15;
+    const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LD + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+    float psum = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++) {
+        h8 pb[2];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float pv = fast_exp2(fmaf(sacc[kt][i], c, -m_use));
+            psum += pv;
+            pb[i >> 3][i & 7] = (_Float16)pv;
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int u = 2 * kt + hh; // 16-key group: keys 16u + 4g + {0..3, 8..11}
+#pragma unroll
+            for (int dt = 0; dt < C::NDT; dt++) {
+                const _Float16* base = vrow + (16 * u) * C::LD + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LD);
+                h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[dt] = mfma_32x32x16_f16(a, pb[hh], oacc[dt]);
+            }
+        }
+    }
+    l_run += psum;
 }
 
 template <int D>
 __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_prefill(PrefillParams p) {
     using C = PrefillCfg<D>;
-    __shared__ __attribute__((aligned(16))) _Float16 sK[kBN * C::K_LD];
-    __shared__ __attribute__((aligned(16))) _Float16 sVT[D * C::VT_LD];
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::BUF_ELEMS];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -84,8 +181,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     const int g = lane >> 5;
 
     // workgroup -> (head group, row tile); the last (heaviest under a causal
-    // mask) row tiles are issued first, head groups fastest so consecutive
-    // workgroups -- and therefore one XCD -- keep sharing K/V of a kv head
+    // mask) row tiles are issued first, head groups fastest so that
+    // workgroups on one XCD keep sharing the K/V of a kv head
     const int wg = blockIdx.x;
     const int hg = wg % p.n_head_groups;
     const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
@@ -116,7 +213,7 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
             h8 x = {};
             if (valid) {
                 x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-                if (p.has_rope) {
+                if (p.rope_q) {
                     x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
                 }
                 if (p.q_sign < 0.0f) {
@@ -146,173 +243,427 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     float l_run = 0.0f;
 
     h8 kreg[C::KT];
-    h8 vreg[C::VT][4];
+    h8 vreg[C::KT];
     const int Sk = p.mask.sk;
+    int row_lo, row_hi;
+    row_key_bounds(p.mask, q, row_lo, row_hi);
 
+    // per-thread chunk of a tile: row e / KCH, 16-byte column e % KCH
+    uint32_t koff[C::KT];
+    uint32_t voff[C::KT];
+    int loff[C::KT];
+#pragma unroll
+    for (int it = 0; it < C::KT; it++) {
+        const int e = tid + it * kThreads;
+        const bool ok = C::TASK % kThreads == 0 || e < C::TASK;
+        const int row = ok ? e / C::KCH : 0;
+        const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
+        koff[it] = (uint32_t)(((int64_t)row * p.k_ss + 8 * ch) * 2);
+        voff[it] = (uint32_t)(((int64_t)row * p.v_ss + 8 * ch) * 2);
+        loff[it] = ok ? row * C::LD + 8 * ch : -1;
+    }
+
+    // HBM -> registers for tile t.  The buffer resources are rebased to the
+    // tile; rows past Sk fall outside num_records and read as 0.
     auto load_kv = [&](int t) {
         const int kt0 = t * kBN;
+        const auto rk = make_rsrc(kbase + (int64_t)kt0 * p.k_ss, range_bytes(Sk - kt0, p.k_ss * 2, D * 2));
+        const auto rv = make_rsrc(vbase + (int64_t)kt0 * p.v_ss, range_bytes(Sk - kt0, p.v_ss * 2, D * 2));
 #pragma unroll
         for (int it = 0; it < C::KT; it++) {
-            const int e = tid + it * kThreads;
-            h8 x = {};
-            if (e < C::KTASK) {
-                const int row = e / C::KCH;
-                const int ch = e - row * C::KCH;
-                const int key = kt0 + row;
-                if (key < Sk) {
-                    x = *reinterpret_cast<const h8*>(kbase + (int64_t)key * p.k_ss + 8 * ch);
-                }
-            }
-            kreg[it] = x;
-        }
-#pragma unroll
-        for (int it = 0; it < C::VT; it++) {
-            const int e = tid + it * kThreads;
-            const int kq = e & 15;
-            const int dc = e >> 4;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                h8 x = {};
-                const int key = kt0 + 4 * kq + r;
-                if (e < C::VTASK && key < Sk) {
-                    x = *reinterpret_cast<const h8*>(vbase + (int64_t)key * p.v_ss + 8 * dc);
-                }
-                vreg[it][r] = x;
-            }
+            kreg[it] = buffer_load_h8(rk, koff[it], 0);
+            vreg[it] = buffer_load_h8(rv, voff[it], 0);
         }
     };
 
-    auto store_kv = [&](int t) {
-        const int kt0 = t * kBN;
+    // registers -> LDS buffer `buf` (K tile, then V tile, both row-major)
+    auto store_kv = [&](int buf) {
+        _Float16* sK = smem + buf * C::BUF_ELEMS;
+        _Float16* sV = sK + C::TILE_ELEMS;
 #pragma unroll
         for (int it = 0; it < C::KT; it++) {
-            const int e = tid + it * kThreads;
-            if (e < C::KTASK) {
-                const int row = e / C::KCH;
-                const int ch = e - row * C::KCH;
-                const int key = kt0 + row;
-                h8 x = kreg[it];
-                if (p.has_rope && key < Sk) {
-                    x = rope8(x, p.rot_cos + (int64_t)key * (D / 2), p.rot_sin + (int64_t)key * (D / 2), 4 * ch);
-                }
-                *reinterpret_cast<h8*>(&sK[row * C::K_LD + 8 * ch]) = x;
-            }
-        }
-#pragma unroll
-        for (int it = 0; it < C::VT; it++) {
-            const int e = tid + it * kThreads;
-            if (e < C::VTASK) {
-                const int kq = e & 15;
-                const int dc = e >> 4;
-                const int pos = (kq >> 2) * 16 + vt_quad_pos(kq & 3) * 4;
-#pragma unroll
-                for (int c = 0; c < 8; c++) {
-                    h4 t4 = {vreg[it][0][c], vreg[it][1][c], vreg[it][2][c], vreg[it][3][c]};
-                    *reinterpret_cast<h4*>(&sVT[(8 * dc + c) * C::VT_LD + pos]) = t4;
-                }
+            if (C::TASK % kThreads == 0 || loff[it] >= 0) {
+                *reinterpret_cast<h8*>(&sK[loff[it]]) = kreg[it];
+                *reinterpret_cast<h8*>(&sV[loff[it]]) = vreg[it];
             }
         }
     };
 
     if (t_begin < t_end) {
         load_kv(t_begin);
+        store_kv(0);
+        if (t_begin + 1 < t_end) {
+            load_kv(t_begin + 1);
+        }
     }
+    __syncthreads();
     for (int t = t_begin; t < t_end; t++) {
-        __syncthreads(); // every wave is done reading the previous tile
-        store_kv(t);
-        __syncthreads();
-        if (t + 1 < t_end) {
-            load_kv(t + 1); // in flight while this tile computes
-        }
-        if (!wave_active) {
-            continue;
-        }
+        const int buf = (t - t_begin) & 1;
+        // stage tile t+1 into the other buffer (free since the last barrier)
+        // and start loading tile t+2
+        auto prefetch = [&]() {
+            if (t + 1 < t_end) {
+                store_kv(buf ^ 1);
+                if (t + 2 < t_end) {
+                    load_kv(t + 2);
+                }
+            }
+        };
         const int kt0 = t * kBN;
-        const int cls = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
-        if (cls == 0) {
-            continue;
+        const int cls = wave_active ? classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1) : 0;
+        const _Float16* sK = smem + buf * C::BUF_ELEMS;
+        const _Float16* sV = sK + C::TILE_ELEMS;
+        if (cls == 1) {
+            tile_step<D, false>(sK, sV, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c, lane, prefetch);
+        } else if (cls == 2) {
+            tile_step<D, true>(sK, sV, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c, lane, prefetch);
+        } else {
+            prefetch();
         }
-
-        // ---- S^T[key][query] = K Q^T, two 32-key halves
-        f16x sacc[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-            f16x acc = {};
-#pragma unroll
-            for (int s = 0; s < C::NS; s++) {
-                h8 a = *reinterpret_cast<const h8*>(&sK[(kt * 32 + l32) * C::K_LD + 16 * s + 8 * g]);
-                acc = mfma_32x32x16_f16(a, qreg[s], acc);
-            }
-            sacc[kt] = acc;
-        }
-
-        // ---- online softmax (log2 domain)
-        if (cls == 2) {
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int key = kt0 + kt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                    if (!key_visible(p.mask, q, key)) {
-                        sacc[kt][i] = -INFINITY;
-                    }
-                }
-            }
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                mx = fmaxf(mx, sacc[kt][i]);
-            }
-        }
-        mx = fmaxf(mx, swap_halves(mx));
-        const float mt = (mx == -INFINITY) ? -INFINITY : mx * p.c;
-        const float m_new = fmaxf(m_run, mt);
-        const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
-
-        h8 pb[4];
-        float psum = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float s = sacc[kt][i];
-                float pv = fast_exp2(fmaf(s, p.c, -m_use));
-                if (cls == 2 && s == -INFINITY) {
-                    pv = 0.0f;
-                }
-                psum += pv;
-                pb[kt * 2 + (i >> 3)][i & 7] = (_Float16)pv;
-            }
-        }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (wave_any(alpha != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-                oacc[dt] *= alpha;
-            }
-        }
-
-        // ---- O^T[d][query] += V^T P^T
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                h8 a = *reinterpret_cast<const h8*>(&sVT[(dt * 32 + l32) * C::VT_LD + u * 16 + 8 * g]);
-                oacc[dt] = mfma_32x32x16_f16(a, pb[u], oacc[dt]);
-            }
-        }
+        __syncthreads();
     }
 
     if (!wave_active) {
         return;
     }
     // ---- normalise once in fp32, round once to fp16
-    const float l = l_run + swap_halves(l_run);
+    const float l = pair_sum(l_run);
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (q < p.Sq) {
+        _Float16* orow = obase + (int64_t)q * p.o_ss;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; dt++) {
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
+                         (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
+                *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong prefill (D <= 128): 8 waves in two groups that alternate between
+// an MFMA phase and a VALU phase, barrier to barrier, so every SIMD always has
+// one wave feeding the matrix core while its partner runs the softmax:
+//
+//   group A:  M(0) V(0) M(1) V(1) ... M(n-1) V(n-1) M(n)  -
+//   group B:  -    M(0) V(0) M(1) ...        M(n-1) V(n-1) M(n)
+//
+//   M(i): S(i) = K(i) Q^T and O += V(i-1)^T P(i-1)     (32 MFMAs at D=128)
+//   V(i): online softmax of S(i) -> P(i), rescale of O, and staging of the
+//         group's half of the next K/V tiles (registers -> LDS, HBM -> regs)
+//
+// K(i) and V(i-1) are read in global phases 2i and 2i+1 and live in LDS slot
+// i % 2 and (i - 1) % 2.  Group A stages pair (K(i+1), V(i)) in its V(i)
+// (phase 2i+1), group B stages pair (K(i+2), V(i+1)) in its V(i) (phase 2i+2);
+// both write slots whose last readers finished before the preceding barrier.
+// ---------------------------------------------------------------------------
+constexpr int kPPWaves = 8;
+constexpr int kPPThreads = 64 * kPPWaves;
+
+template <int D>
+struct PPCfg {
+    static constexpr int LD = D + 16;                  // LDS row stride (halves)
+    static constexpr int TILE_ELEMS = kBN * LD;
+    static constexpr int NS = D / 16;
+    static constexpr int NDT = D / 32;
+    static constexpr int KCH = D / 8;
+    static constexpr int HALF_TASK = 32 * KCH;         // one group's chunks of one K (or V) tile
+    static constexpr int CT = (HALF_TASK + 255) / 256; // K (and V) chunks per thread
+};
+
+template <int D>
+__global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) {
+    using C = PPCfg<D>;
+    // sK[slot], sV[slot]
+    __shared__ __attribute__((aligned(16))) _Float16 smem[4 * C::TILE_ELEMS];
+    _Float16* const sKs = smem;
+    _Float16* const sVs = smem + 2 * C::TILE_ELEMS;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6;
+    const int lane = tid & 63;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int grp = wave >> 2;       // 0 = group A, 1 = group B
+    const int gtid = tid & 255;      // thread index inside the group
+
+    const int wg = blockIdx.x;
+    const int hg = wg % p.n_head_groups;
+    const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
+    const int per_b = p.Hkv * p.groups_per_kv;
+    const int b = hg / per_b;
+    const int rem = hg - b * per_b;
+    const int kvh = rem / p.groups_per_kv;
+    const int sub = rem - kvh * p.groups_per_kv;
+    const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
+    const int wg_q0 = rt * p.rows_per_wg;
+    const int q0 = wg_q0 + (wave / p.G) * 32;
+    const int q = q0 + l32;
+    const bool wave_active = q0 < p.Sq;
+    const int q_hi = min(q0 + 31, p.Sq - 1);
+
+    const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
+    const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
+    const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
+    _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
+
+    h8 qreg[C::NS];
+    {
+        const bool valid = q < p.Sq;
+        const _Float16* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
+#pragma unroll
+        for (int s = 0; s < C::NS; s++) {
+            h8 x = {};
+            if (valid) {
+                x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
+                if (p.rope_q) {
+                    x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
+                }
+                if (p.q_sign < 0.0f) {
+                    x = -x;
+                }
+            }
+            qreg[s] = x;
+        }
+    }
+
+    const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
+    int klo, khi;
+    visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
+    int t_begin = 0, n = 0;
+    if (khi >= klo) {
+        t_begin = klo / kBN;
+        n = khi / kBN + 1 - t_begin;
+    }
+    const int Sk = p.mask.sk;
+    int row_lo, row_hi;
+    row_key_bounds(p.mask, q, row_lo, row_hi);
+
+    f16x oacc[C::NDT];
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; dt++) {
+        oacc[dt] = f16x{};
+    }
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    f16x sacc[2];
+    sacc[0] = f16x{};
+    sacc[1] = f16x{};
+    h8 pb[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        pb[u] = h8{};
+    }
+    int cls_prev = 0; // classification of the tile whose P is held in pb
+
+    // ---- staging: this group's half (rows 32*grp .. +31) of K(x) and V(x-1)
+    h8 kreg[C::CT], vreg[C::CT];
+    uint32_t coff_k[C::CT], coff_v[C::CT];
+    int cl[C::CT]; // LDS element offset inside a tile, -1 = no chunk
+#pragma unroll
+    for (int it = 0; it < C::CT; it++) {
+        const int e = gtid + it * 256;
+        const bool ok = C::HALF_TASK % 256 == 0 || e < C::HALF_TASK;
+        const int row = 32 * grp + (ok ? e / C::KCH : 0);
+        const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
+        coff_k[it] = (uint32_t)(((int64_t)row * p.k_ss + 8 * ch) * 2);
+        coff_v[it] = (uint32_t)(((int64_t)row * p.v_ss + 8 * ch) * 2);
+        cl[it] = ok ? row * C::LD + 8 * ch : -1;
+    }
+    // registers <- HBM for pair x (K tile x if x < n, V tile x-1 if 1 <= x <= n);
+    // a missing tile gets num_records 0, so its loads return 0 and touch nothing
+    auto load_pair = [&](int x) {
+        const int tk = t_begin + x, tv = t_begin + x - 1;
+        const auto rk = make_rsrc(kbase + (int64_t)tk * kBN * p.k_ss,
+                                  x < n ? range_bytes(Sk - tk * kBN, p.k_ss * 2, D * 2) : 0u);
+        const auto rv = make_rsrc(vbase + (int64_t)tv * kBN * p.v_ss,
+                                  (x >= 1 && x <= n) ? range_bytes(Sk - tv * kBN, p.v_ss * 2, D * 2) : 0u);
+#pragma unroll
+        for (int it = 0; it < C::CT; it++) {
+            kreg[it] = buffer_load_h8(rk, coff_k[it], 0);
+            vreg[it] = buffer_load_h8(rv, coff_v[it], 0);
+        }
+    };
+    // LDS <- registers for pair x
+    auto store_pair = [&](int x) {
+        _Float16* sK = sKs + (x & 1) * C::TILE_ELEMS;
+        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_ELEMS;
+#pragma unroll
+        for (int it = 0; it < C::CT; it++) {
+            if (C::HALF_TASK % 256 == 0 || cl[it] >= 0) {
+                if (x < n) {
+                    *reinterpret_cast<h8*>(&sK[cl[it]]) = kreg[it];
+                }
+                if (x >= 1 && x <= n) {
+                    *reinterpret_cast<h8*>(&sV[cl[it]]) = vreg[it];
+                }
+            }
+        }
+    };
+
+    // M(i): S(i) = K(i) Q^T (i < n) and O += V(i-1)^T P(i-1) (i >= 1).
+    // Software-pipelined in steps of two MFMAs: the LDS operands of step j+1
+    // are read while step j's MFMAs issue; sched_barrier keeps the compiler
+    // from hoisting every read (which would need ~100 extra VGPRs).
+    auto phase_m = [&](int i) {
+        if (!wave_active) {
+            return;
+        }
+        const bool do_pv = i >= 1 && cls_prev != 0;
+        int cls_now = 0;
+        if (i < n) {
+            const int kt0 = (t_begin + i) * kBN;
+            cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
+        }
+        if (do_pv) {
+            const _Float16* sV = sVs + ((i - 1) & 1) * C::TILE_ELEMS;
+            const int j16 = lane & 15;
+            const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LD + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+            constexpr int NSTEP = 4 * C::NDT; // (u, dt)
+            auto vop = [&](int st) {
+                const int u = st / C::NDT, dt = st % C::NDT;
+                const _Float16* base = vrow + (16 * u) * C::LD + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LD);
+                return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            };
+            h8 cur = vop(0);
+#pragma unroll
+            for (int st = 0; st < NSTEP; st++) {
+                h8 nxt = cur;
+                if (st + 1 < NSTEP) {
+                    nxt = vop(st + 1);
+                }
+                oacc[st % C::NDT] = mfma_32x32x16_f16(cur, pb[st / C::NDT], oacc[st % C::NDT]);
+                __builtin_amdgcn_sched_barrier(0);
+                cur = nxt;
+            }
+        }
+        if (cls_now != 0) {
+            const _Float16* sK = sKs + (i & 1) * C::TILE_ELEMS;
+            const _Float16* krow = sK + l32 * C::LD + 8 * g;
+            f16x acc0 = {}, acc1 = {};
+            h8 a0 = *reinterpret_cast<const h8*>(krow);
+            h8 a1 = *reinterpret_cast<const h8*>(krow + 32 * C::LD);
+#pragma unroll
+            for (int st = 0; st < C::NS; st++) {
+                h8 n0 = a0, n1 = a1;
+                if (st + 1 < C::NS) {
+                    n0 = *reinterpret_cast<const h8*>(krow + 16 * (st + 1));
+                    n1 = *reinterpret_cast<const h8*>(krow + 32 * C::LD + 16 * (st + 1));
+                }
+                acc0 = mfma_32x32x16_f16(a0, qreg[st], acc0);
+                acc1 = mfma_32x32x16_f16(a1, qreg[st], acc1);
+                __builtin_amdgcn_sched_barrier(0);
+                a0 = n0;
+                a1 = n1;
+            }
+            sacc[0] = acc0;
+            sacc[1] = acc1;
+        }
+        cls_prev = cls_now;
+    };
+
+    // V(i): softmax of S(i) -> pb, rescale O
+    auto phase_v = [&](int i) {
+        if (!wave_active || cls_prev == 0) {
+            return;
+        }
+        if (cls_prev == 2) {
+            const int kt0 = (t_begin + i) * kBN;
+            const int a = row_lo - kt0 - 4 * g;
+            const int bnd = row_hi - kt0 - 4 * g;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
+                    sacc[kt][e] = (off < a || off > bnd) ? -INFINITY : sacc[kt][e];
+                }
+            }
+        }
+        float mx = sacc[0][0];
+#pragma unroll
+        for (int e = 1; e < 16; e++) {
+            mx = fmaxf(mx, sacc[0][e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            mx = fmaxf(mx, sacc[1][e]);
+        }
+        mx = pair_max(mx);
+        const float m_new = fmaxf(m_run, mx * p.c);
+        const bool grow = m_new > m_run + kRescaleThreshold;
+        if (wave_any(grow)) {
+            const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+            if (grow) {
+                m_run = m_new;
+            }
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < C::NDT; dt++) {
+                oacc[dt] *= alpha;
+            }
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        float psum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float pv = fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
+                psum += pv;
+                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)pv;
+            }
+        }
+        l_run += psum;
+    };
+
+    // ---- prologue: pair 0 in LDS; each group's registers hold its next pair
+    if (n > 0) {
+        load_pair(0);
+        store_pair(0);
+        load_pair(1);
+    }
+    __syncthreads();
+    // Both groups pass 2n + 2 barriers; group B starts one phase late.
+    if (n > 0) {
+        if (grp == 0) {
+            for (int i = 0; i < n; i++) {
+                phase_m(i);
+                __syncthreads();
+                store_pair(i + 1);
+                load_pair(i + 2);
+                phase_v(i);
+                __syncthreads();
+            }
+            phase_m(n);
+            __syncthreads();
+            __syncthreads();
+        } else {
+            store_pair(1);
+            load_pair(2);
+            __syncthreads();
+            for (int i = 0; i < n; i++) {
+                phase_m(i);
+                __syncthreads();
+                store_pair(i + 2);
+                load_pair(i + 3);
+                phase_v(i);
+                __syncthreads();
+            }
+            phase_m(n);
+            __syncthreads();
+        }
+    }
+
+    if (!wave_active) {
+        return;
+    }
+    const float l = pair_sum(l_run);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     if (q < p.Sq) {
         _Float16* orow = obase + (int64_t)q * p.o_ss;
@@ -329,6 +680,17 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
 }
 
 template <int D>
+int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    hipLaunchKernelGGL(fa_fwd_f16_pp<D>, dim3((uint32_t)n_wg), dim3(kPPThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        err = hipGetErrorString(e);
+        return -1;
+    }
+    return 0;
+}
+
+template <int D>
 int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     hipLaunchKernelGGL(fa_fwd_f16_prefill<D>, dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
@@ -341,7 +703,13 @@ int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std
 
 } // namespace
 
-int fwd_f16_prefill(const AttnArgs& a, hipStream_t stream, std::string& err) {
+constexpr int64_t kMaxSeqStride = 1 << 24;
+
+float softmax_log2_scale(float scale) {
+    return std::max(std::fabs(scale) * kLog2e, 1e-30f);
+}
+
+int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err) {
     PrefillParams p{};
     p.q = static_cast<const _Float16*>(a.q);
     p.k = static_cast<const _Float16*>(a.k);
@@ -365,14 +733,15 @@ int fwd_f16_prefill(const AttnArgs& a, hipStream_t stream, std::string& err) {
     p.Hkv = a.Hkv;
     p.ratio = a.Hq / a.Hkv;
     p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
-    p.rows_per_wg = 32 * kWaves / p.G;
+    const bool pp = a.D <= 128;
+    p.rows_per_wg = 32 * (pp ? kPPWaves : kWaves) / p.G;
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
     p.n_head_groups = a.B * a.Hkv * p.groups_per_kv;
-    p.c = std::fabs(a.scale) * kLog2e;
+    p.c = softmax_log2_scale(a.scale);
     p.q_sign = a.scale < 0.0f ? -1.0f : 1.0f;
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};
-    p.has_rope = a.has_rope ? 1 : 0;
+    p.rope_q = rope_q ? 1 : 0;
 
     const int64_t n_wg = (int64_t)p.n_row_tiles * p.n_head_groups;
     if (n_wg <= 0) {
@@ -384,10 +753,10 @@ int fwd_f16_prefill(const AttnArgs& a, hipStream_t stream, std::string& err) {
         return -1;
     }
     switch (a.D) {
-    case 32: return launch_prefill<32>(p, n_wg, stream, err);
-    case 64: return launch_prefill<64>(p, n_wg, stream, err);
-    case 96: return launch_prefill<96>(p, n_wg, stream, err);
-    case 128: return launch_prefill<128>(p, n_wg, stream, err);
+    case 32: return launch_pp<32>(p, n_wg, stream, err);
+    case 64: return launch_pp<64>(p, n_wg, stream, err);
+    case 96: return launch_pp<96>(p, n_wg, stream, err);
+    case 128: return launch_pp<128>(p, n_wg, stream, err);
     case 160: return launch_prefill<160>(p, n_wg, stream, err);
     case 192: return launch_prefill<192>(p, n_wg, stream, err);
     case 224: return launch_prefill<224>(p, n_wg, stream, err);
@@ -398,17 +767,27 @@ int fwd_f16_prefill(const AttnArgs& a, hipStream_t stream, std::string& err) {
     return -1;
 }
 
-} // namespace rdna_amd
-
-namespace rdna_amd {
-
-int fwd_f16_splitk(const AttnArgs& a, hipStream_t stream, std::string& err);
-
-int fwd_f16(const AttnArgs& a, F16Path path, hipStream_t stream, std::string& err) {
-    if (path == F16Path::SplitK) {
-        return fwd_f16_splitk(a, stream, err);
+int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& err) {
+    AttnArgs a = in;
+    // K/V rows are addressed with 32-bit byte offsets inside a 64-key tile
+    if (a.ks[2] < 0 || a.vs[2] < 0 || a.ks[2] > kMaxSeqStride || a.vs[2] > kMaxSeqStride) {
+        err = "key/value seq strides must be in [0, 2^24] elements";
+        return -1;
     }
-    return fwd_f16_prefill(a, stream, err);
+    const bool splitk = path == F16Path::SplitK;
+    StreamScratch krot;
+    if (a.has_rope && a.Sk > 0) {
+        const size_t bytes = (size_t)a.B * a.Hkv * a.Sk * a.D * sizeof(_Float16);
+        if (krot.alloc(bytes, stream, err) != 0 || rope_rotate_k(a, krot.ptr, stream, err) != 0) {
+            return -1;
+        }
+        a.k = krot.ptr;
+        a.ks[0] = (int64_t)a.Hkv * a.Sk * a.D;
+        a.ks[1] = (int64_t)a.Sk * a.D;
+        a.ks[2] = a.D;
+    }
+    return splitk ? fwd_f16_splitk(a, a.has_rope != 0, stream, err)
+                  : fwd_f16_prefill(a, a.has_rope != 0, stream, err);
 }
 
 } // namespace rdna_amd

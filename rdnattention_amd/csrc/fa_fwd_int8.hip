@@ -1,5 +1,6 @@
 // INT8 forward (placeholder until the int8 MFMA kernel lands).
 #include "fa_host.hpp"
+#include "fa_internal.hpp"
 
 namespace rdna_amd {
 
@@ -13,7 +14,7 @@ int int8_scores(const AttnArgs&, int32_t*, hipStream_t, std::string& err) {
     return -1;
 }
 
-int fwd_f16_splitk(const AttnArgs&, hipStream_t, std::string& err) {
+int fwd_f16_splitk(const AttnArgs&, bool, hipStream_t, std::string& err) {
     err = "split-K path not built";
     return -1;
 }
