@@ -10,9 +10,9 @@
 // before any HIP call: head_dim, the GQA ratio, empty grids, null pointers,
 // 16-byte alignment of pointers and strides (the reference's 128-bit loads
 // assumed it silently), RoPE tables, and int32 index ranges.
-#include "../../include/rdnattention.h"
-#include "../../include/rdnattention.hpp"
-#include "../../include/rdnattention_ext.h"
+#include "rdnattention.h"
+#include "rdnattention.hpp"
+#include "rdnattention_ext.h"
 #include "fa_host.hpp"
 
 #include <hip/hip_runtime.h>

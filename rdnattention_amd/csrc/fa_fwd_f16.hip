@@ -28,6 +28,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace rdna_amd {
 namespace {
@@ -361,12 +362,18 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
 // both write slots whose last readers finished before the preceding barrier.
 // ---------------------------------------------------------------------------
 constexpr int kPPWaves = 8;
+constexpr int kOpDepth = 4; // MFMA operands in flight in the MFMA phase
 constexpr int kPPThreads = 64 * kPPWaves;
 
 template <int D>
 struct PPCfg {
-    static constexpr int LD = D + 16;                  // LDS row stride (halves)
-    static constexpr int TILE_ELEMS = kBN * LD;
+    // LDS row strides (64 banks x 4 B): K rows are read 16 at a time with
+    // ds_read_b128 -> a 16 B step mod 256 B keeps them in distinct banks; V rows
+    // are read 4 at a time, 64 B each, by the transpose read -> a 64 B step
+    static constexpr int LDK = D + 8;
+    static constexpr int LDV = D + 32;
+    static constexpr int TILE_K = kBN * LDK;
+    static constexpr int TILE_V = kBN * LDV;
     static constexpr int NS = D / 16;
     static constexpr int NDT = D / 32;
     static constexpr int KCH = D / 8;
@@ -378,9 +385,9 @@ template <int D>
 __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) {
     using C = PPCfg<D>;
     // sK[slot], sV[slot]
-    __shared__ __attribute__((aligned(16))) _Float16 smem[4 * C::TILE_ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::TILE_K + 2 * C::TILE_V];
     _Float16* const sKs = smem;
-    _Float16* const sVs = smem + 2 * C::TILE_ELEMS;
+    _Float16* const sVs = smem + 2 * C::TILE_K;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -462,7 +469,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     // ---- staging: this group's half (rows 32*grp .. +31) of K(x) and V(x-1)
     h8 kreg[C::CT], vreg[C::CT];
     uint32_t coff_k[C::CT], coff_v[C::CT];
-    int cl[C::CT]; // LDS element offset inside a tile, -1 = no chunk
+    int clk[C::CT], clv[C::CT]; // LDS element offsets inside a tile, -1 = no chunk
 #pragma unroll
     for (int it = 0; it < C::CT; it++) {
         const int e = gtid + it * 256;
@@ -471,7 +478,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
         coff_k[it] = (uint32_t)(((int64_t)row * p.k_ss + 8 * ch) * 2);
         coff_v[it] = (uint32_t)(((int64_t)row * p.v_ss + 8 * ch) * 2);
-        cl[it] = ok ? row * C::LD + 8 * ch : -1;
+        clk[it] = ok ? row * C::LDK + 8 * ch : -1;
+        clv[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
     // registers <- HBM for pair x (K tile x if x < n, V tile x-1 if 1 <= x <= n);
     // a missing tile gets num_records 0, so its loads return 0 and touch nothing
@@ -489,25 +497,77 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     };
     // LDS <- registers for pair x
     auto store_pair = [&](int x) {
-        _Float16* sK = sKs + (x & 1) * C::TILE_ELEMS;
-        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_ELEMS;
+        _Float16* sK = sKs + (x & 1) * C::TILE_K;
+        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
 #pragma unroll
         for (int it = 0; it < C::CT; it++) {
-            if (C::HALF_TASK % 256 == 0 || cl[it] >= 0) {
+            if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
                 if (x < n) {
-                    *reinterpret_cast<h8*>(&sK[cl[it]]) = kreg[it];
+                    *reinterpret_cast<h8*>(&sK[clk[it]]) = kreg[it];
                 }
                 if (x >= 1 && x <= n) {
-                    *reinterpret_cast<h8*>(&sV[cl[it]]) = vreg[it];
+                    *reinterpret_cast<h8*>(&sV[clv[it]]) = vreg[it];
                 }
             }
         }
     };
 
-    // M(i): S(i) = K(i) Q^T (i < n) and O += V(i-1)^T P(i-1) (i >= 1).
-    // Software-pipelined in steps of two MFMAs: the LDS operands of step j+1
-    // are read while step j's MFMAs issue; sched_barrier keeps the compiler
-    // from hoisting every read (which would need ~100 extra VGPRs).
+    // M(i): O += V(i-1)^T P(i-1) (i >= 1) then S(i) = K(i) Q^T (i < n), as one
+    // stream of MFMAs whose LDS operands are read kOpDepth MFMAs ahead through
+    // a small register ring; sched_barrier stops the compiler from hoisting
+    // every read (which would need ~100 more VGPRs).
+    auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+        constexpr bool DO_PV = decltype(do_pv_c)::value;
+        constexpr bool DO_S = decltype(do_s_c)::value;
+        constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
+        constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
+        constexpr int T = NPV + NSK;
+        constexpr int DEPTH = T < kOpDepth ? T : kOpDepth;
+        const int j16 = lane & 15;
+        const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
+                               16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+        const _Float16* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 8 * g;
+        auto op = [&](int j) -> h8 {
+            if (j < NPV) {
+                const int u = j / C::NDT, dt = j % C::NDT;
+                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+            const int js = j - NPV, st = js >> 1, kt = js & 1;
+            return *reinterpret_cast<const h8*>(krow + kt * 32 * C::LDK + 16 * st);
+        };
+        f16x acc0 = {}, acc1 = {};
+        h8 ring[DEPTH > 0 ? DEPTH : 1];
+#pragma unroll
+        for (int j = 0; j < DEPTH; j++) {
+            ring[j] = op(j);
+        }
+#pragma unroll
+        for (int j = 0; j < T; j++) {
+            const h8 a = ring[j % DEPTH];
+            if (j + DEPTH < T) {
+                ring[j % DEPTH] = op(j + DEPTH);
+            }
+            if (j < NPV) {
+                const int u = j / C::NDT, dt = j % C::NDT;
+                oacc[dt] = mfma_32x32x16_f16(a, pb[u], oacc[dt]);
+            } else {
+                const int js = j - NPV, st = js >> 1;
+                if (js & 1) {
+                    acc1 = mfma_32x32x16_f16(a, qreg[st], acc1);
+                } else {
+                    acc0 = mfma_32x32x16_f16(a, qreg[st], acc0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (DO_S) {
+            sacc[0] = acc0;
+            sacc[1] = acc1;
+        }
+    };
     auto phase_m = [&](int i) {
         if (!wave_active) {
             return;
@@ -518,51 +578,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             const int kt0 = (t_begin + i) * kBN;
             cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
         }
-        if (do_pv) {
-            const _Float16* sV = sVs + ((i - 1) & 1) * C::TILE_ELEMS;
-            const int j16 = lane & 15;
-            const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LD + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-            constexpr int NSTEP = 4 * C::NDT; // (u, dt)
-            auto vop = [&](int st) {
-                const int u = st / C::NDT, dt = st % C::NDT;
-                const _Float16* base = vrow + (16 * u) * C::LD + 32 * dt;
-                h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LD);
-                return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            };
-            h8 cur = vop(0);
-#pragma unroll
-            for (int st = 0; st < NSTEP; st++) {
-                h8 nxt = cur;
-                if (st + 1 < NSTEP) {
-                    nxt = vop(st + 1);
-                }
-                oacc[st % C::NDT] = mfma_32x32x16_f16(cur, pb[st / C::NDT], oacc[st % C::NDT]);
-                __builtin_amdgcn_sched_barrier(0);
-                cur = nxt;
-            }
-        }
-        if (cls_now != 0) {
-            const _Float16* sK = sKs + (i & 1) * C::TILE_ELEMS;
-            const _Float16* krow = sK + l32 * C::LD + 8 * g;
-            f16x acc0 = {}, acc1 = {};
-            h8 a0 = *reinterpret_cast<const h8*>(krow);
-            h8 a1 = *reinterpret_cast<const h8*>(krow + 32 * C::LD);
-#pragma unroll
-            for (int st = 0; st < C::NS; st++) {
-                h8 n0 = a0, n1 = a1;
-                if (st + 1 < C::NS) {
-                    n0 = *reinterpret_cast<const h8*>(krow + 16 * (st + 1));
-                    n1 = *reinterpret_cast<const h8*>(krow + 32 * C::LD + 16 * (st + 1));
-                }
-                acc0 = mfma_32x32x16_f16(a0, qreg[st], acc0);
-                acc1 = mfma_32x32x16_f16(a1, qreg[st], acc1);
-                __builtin_amdgcn_sched_barrier(0);
-                a0 = n0;
-                a1 = n1;
-            }
-            sacc[0] = acc0;
-            sacc[1] = acc1;
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (do_pv && cls_now != 0) {
+            mfma_stream(T_{}, T_{}, i);
+        } else if (do_pv) {
+            mfma_stream(T_{}, F_{}, i);
+        } else if (cls_now != 0) {
+            mfma_stream(F_{}, T_{}, i);
         }
         cls_prev = cls_now;
     };
