@@ -71,6 +71,15 @@ __device__ __forceinline__ float pair_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
+// [6:4], lgkmcnt [11:8]); the counters not named are left unwaited.
+constexpr int waitcnt_vm(int n) {
+    return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8);
+}
+constexpr int waitcnt_lgkm(int n) {
+    return 0xf | (0x3 << 14) | (0x7 << 4) | ((n & 0xf) << 8);
+}
+
 __device__ __forceinline__ bool wave_any(bool pred) {
     return __builtin_amdgcn_ballot_w64(pred) != 0;
 }
@@ -166,6 +175,29 @@ __device__ __forceinline__ h8 buffer_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t 
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
     u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
     return __builtin_bit_cast(h8, x);
+}
+
+// HBM -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds): lane i
+// reads the buffer at voff and writes LDS bytes [lds + 16 i, lds + 16 i + 16).
+// Issued from inline asm so the compiler's waitcnt insertion does not treat it
+// as a store to every LDS location (it would otherwise wait for all of them
+// before each LDS read); callers wait on vmcnt themselves.  The V# is built
+// by hand: base, stride 0, num_records, DATA_FORMAT 32.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t make_rsrc_v(const void* base, uint32_t num_records) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4_t r;
+    r[0] = (int)(uint32_t)a;
+    r[1] = (int)(uint32_t)(a >> 32);
+    r[2] = (int)num_records;
+    r[3] = 0x00020000;
+    return r;
+}
+__device__ __forceinline__ void dma_load16(i32x4_t rsrc, uint32_t voff, uint32_t lds_byte_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
+                 : "memory", "m0");
 }
 
 // Bytes of a strided row range [row0, n_rows) of a row-major tensor with

@@ -790,6 +790,14 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     return -1;
 }
 
+bool splitk_supported(const AttnArgs& a);
+
+// Auto: few query rows per kv head against a long key sequence -> split-K
+// (HBM-bound, parallel over the key axis); everything else -> prefill tiles.
+bool prefer_splitk(const AttnArgs& a) {
+    return splitk_supported(a) && a.Sk >= 512;
+}
+
 int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& err) {
     AttnArgs a = in;
     // K/V rows are addressed with 32-bit byte offsets inside a 64-key tile
@@ -797,7 +805,7 @@ int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& e
         err = "key/value seq strides must be in [0, 2^24] elements";
         return -1;
     }
-    const bool splitk = path == F16Path::SplitK;
+    const bool splitk = path == F16Path::SplitK || (path == F16Path::Auto && prefer_splitk(a));
     StreamScratch krot;
     if (a.has_rope && a.Sk > 0) {
         const size_t bytes = (size_t)a.B * a.Hkv * a.Sk * a.D * sizeof(_Float16);

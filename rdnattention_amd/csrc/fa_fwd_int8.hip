@@ -14,9 +14,5 @@ int int8_scores(const AttnArgs&, int32_t*, hipStream_t, std::string& err) {
     return -1;
 }
 
-int fwd_f16_splitk(const AttnArgs&, bool, hipStream_t, std::string& err) {
-    err = "split-K path not built";
-    return -1;
-}
 
 } // namespace rdna_amd
