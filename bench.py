@@ -1,25 +1,43 @@
 """Benchmark of the FlashAttention-2 forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                    [--no-cpu] [--no-secondary]
+    python bench.py --copy-calibration          (a plain copy of known size)
+    python bench.py --pmc-summary DIR           (rocprofv3 counter CSVs -> table)
 
 Default workload (the headline metric): FP16 causal GQA prefill with
 in-kernel RoPE (theta 10000), B=4, Hq=32, Hkv=8, S=key_S=4096, D=128,
 Q/K/V ~ N(0,1) fp16 from CPU torch.Generator seed 1, already resident in HBM.
-A "step" is one forward over the whole batch through the C ABI.
+A "step" is one forward over the whole batch through the C ABI (for RoPE
+inputs that is the K pre-rotation kernel plus the attention kernel).
 
-Prints ONE JSON line: value = TFLOP/s over the timed steps (exact masked
-pair count, 4*B*Hq*pairs*D FLOPs), roofline of the attention kernel from
-HIP events on its stream, and a CPU baseline (torch SDPA on host cores on a
-bounded sample of the same workload).
+Prints ONE JSON line:
+  value      TFLOP/s of whole steps (exact masked pair count,
+             4*B*Hq*pairs*D FLOPs) over the timed steps, HIP events on
+             torch's current stream, which the library launches on;
+  roofline   the attention kernel alone: FLOPs (or, for decode, algorithmic
+             bytes) divided by its mean launch time from the library's kernel
+             timer (HIP events recorded around that kernel's launches on its
+             stream); `traffic` = HBM bytes per launch from the committed
+             rocprofv3 FETCH_SIZE/WRITE_SIZE summary for this kernel and
+             workload, scaled by the copy calibration it records, or null;
+  cpu_baseline  the CPU oracle (C, fp64, threaded) on a bounded sample of
+             the same workload on the host cores ("port");
+  cpu_sdpa   torch's CPU scaled_dot_product_attention on a bounded sample;
+  secondary  the other measured shapes: INT8 vs FP16 on the INT8 shape,
+             split-K decode HBM bandwidth, large-head sliding windows.
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import platform
+import re
 import sys
 import time
+from dataclasses import dataclass
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -31,14 +49,67 @@ HBM_PEAK_GBS = 8000.0       # HBM3E
 
 METRIC = "attn fwd TFLOPS (fp16) / TOPS (int8), GQA causal S=4096 D=128; % MFMA peak"
 
+
+@dataclass(frozen=True)
+class Workload:
+    kind: str        # "f16" (prefill), "int8", "decode" (split-K, strided K/V cache views)
+    b: int
+    hq: int
+    hkv: int
+    sq: int
+    sk: int
+    d: int
+    causal: bool
+    window: int
+    rope: bool
+    seed: int
+    std: float
+    kernel: str      # the main kernel, as rocprofv3 names it
+
+    @property
+    def flops(self) -> int:
+        return attn_flops(self.b, self.hq, self.sq, self.sk, self.d, self.causal, self.window)
+
+    @property
+    def io_bytes(self) -> int:
+        """Algorithmic HBM bytes of one forward: Q, K, V and O once each
+        (+ RoPE tables, + per-token scales)."""
+        e = 1 if self.kind == "int8" else 2
+        n = (self.b * self.hq * self.sq * self.d) * (e + 2) + 2 * self.b * self.hkv * self.sk * self.d * e
+        if self.rope:
+            n += 2 * max(self.sq, self.sk) * (self.d // 2) * 4
+        if self.kind == "int8":
+            n += 4 * self.b * (self.hq * self.sq + self.hkv * self.sk)
+        return n
+
+
 WORKLOADS = {
-    # name: (B, Hq, Hkv, Sq, Sk, D, causal, window, rope, seed, std)
-    "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128": (4, 32, 8, 4096, 4096, 128, True, -1, True, 1, 1.0),
-    "fp16_mha_b1_h8_s512_d64": (1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0),
-    "fp16_window4096_rope_b1_h16_s16384_d256": (1, 16, 16, 16384, 16384, 256, False, 4096, True, 4, 0.5),
-    "fp16_window4096_rope_b1_h16_s4096_d512": (1, 16, 16, 4096, 4096, 512, False, 4096, True, 5, 0.5),
+    "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128":
+        Workload("f16", 4, 32, 8, 4096, 4096, 128, True, -1, True, 1, 1.0, "fa_fwd_f16_pp<128>"),
+    "fp16_mha_b1_h8_s512_d64":
+        Workload("f16", 1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0, "fa_fwd_f16_pp<64>"),
+    "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128":
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128>"),
+    "fp16_causal_gqa_b2_h32_kv8_s8192_d128":
+        Workload("f16", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<128>"),
+    "fp16_decode_b16_h32_kv8_sq1_sk32768_d128":
+        Workload("decode", 16, 32, 8, 1, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
+    "fp16_decode_b16_h32_kv8_sq4_sk32768_d128":
+        Workload("decode", 16, 32, 8, 4, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
+    "fp16_window4096_rope_b1_h16_s16384_d256":
+        Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_prefill<256>"),
+    "fp16_window4096_rope_b1_h16_s4096_d512":
+        Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_prefill<512>"),
 }
 DEFAULT = "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128"
+SECONDARY = [
+    "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128",
+    "fp16_causal_gqa_b2_h32_kv8_s8192_d128",
+    "fp16_decode_b16_h32_kv8_sq1_sk32768_d128",
+    "fp16_decode_b16_h32_kv8_sq4_sk32768_d128",
+    "fp16_window4096_rope_b1_h16_s16384_d256",
+    "fp16_window4096_rope_b1_h16_s4096_d512",
+]
 
 
 def cpu_model() -> str:
@@ -53,7 +124,9 @@ def cpu_model() -> str:
 
 def valid_pairs(sq: int, sk: int, causal: bool, window: int) -> int:
     """Exact number of visible (query, key) pairs of one head: the FLOP-count
-    convention of the reference's tests/benchmark.py:77-88, extended to windows."""
+    convention of the reference's tests/benchmark.py:77-88, extended to windows
+    (bottom-right aligned, delta = sk - sq; one-sided causal window w keeps
+    keys with q+delta-k < w, a two-sided one |q+delta-k| <= w/2)."""
     import numpy as np
 
     i = np.arange(sq, dtype=np.int64) + (sk - sq)
@@ -85,7 +158,7 @@ def rope_tables(rows: int, head_dim: int, theta: float = 10000.0):
 
 
 def rope_interleaved(x, cos, sin):
-    """Interleaved-pair RoPE with torch ops (fp32), for the CPU baseline."""
+    """Interleaved-pair RoPE with torch ops (fp32), for the CPU SDPA baseline."""
     s = x.shape[-2]
     c, sn = cos[:s], sin[:s]
     a, b = x[..., 0::2], x[..., 1::2]
@@ -95,124 +168,319 @@ def rope_interleaved(x, cos, sin):
     return y
 
 
-def make_inputs(spec):
+# --------------------------------------------------------------------------- #
+# inputs and one step per workload kind
+# --------------------------------------------------------------------------- #
+def cpu_inputs(wl: Workload):
+    """The headline's inputs: CPU torch.Generator(seed) N(0, std) -> fp16."""
     import torch
 
-    b, hq, hkv, sq, sk, d, causal, window, rope, seed, std = spec
-    g = torch.Generator().manual_seed(seed)
-    q = (torch.randn(b, hq, sq, d, generator=g) * std).half()
-    k = (torch.randn(b, hkv, sk, d, generator=g) * std).half()
-    v = (torch.randn(b, hkv, sk, d, generator=g) * std).half()
+    g = torch.Generator().manual_seed(wl.seed)
+    q = (torch.randn(wl.b, wl.hq, wl.sq, wl.d, generator=g) * wl.std).half()
+    k = (torch.randn(wl.b, wl.hkv, wl.sk, wl.d, generator=g) * wl.std).half()
+    v = (torch.randn(wl.b, wl.hkv, wl.sk, wl.d, generator=g) * wl.std).half()
     cos = sin = None
-    if rope:
-        cos, sin = rope_tables(max(sq, sk), d)
+    if wl.rope:
+        cos, sin = rope_tables(max(wl.sq, wl.sk), wl.d)
     return q, k, v, cos, sin
 
 
-def cpu_baseline(spec, q, k, v, cos, sin, budget_s=20.0):
-    """torch CPU SDPA (fp32) on host cores, on a bounded sample of the workload:
-    one batch element and the query heads of as many kv heads as fit the time
-    budget, full sequence length.  FLOPs counted like the GPU's."""
+def make_step(wl: Workload, dev, host=None):
+    """Device inputs (moved from `host`, or drawn on the GPU from the
+    workload's seed) and a closure running one forward."""
     import torch
 
-    b, hq, hkv, sq, sk, d, causal, window, rope, seed, std = spec
-    ratio = hq // hkv
-    delta = sk - sq
+    import rdnattention_amd as ra
 
-    def run(n_kv):
-        qs = q[:1, : n_kv * ratio].float()
-        ks = k[:1, :n_kv].float()
-        vs = v[:1, :n_kv].float()
-        if rope:
+    g = torch.Generator(device=dev).manual_seed(wl.seed)
+
+    def randn(*shape):
+        return torch.randn(*shape, device=dev, generator=g) * wl.std
+
+    if wl.kind == "f16":
+        if host is not None:
+            q, k, v, cos, sin = host
+            q, k, v = q.to(dev), k.to(dev), v.to(dev)
+        else:
+            q = randn(wl.b, wl.hq, wl.sq, wl.d).half()
+            k = randn(wl.b, wl.hkv, wl.sk, wl.d).half()
+            v = randn(wl.b, wl.hkv, wl.sk, wl.d).half()
+            cos = sin = None
+            if wl.rope:
+                cos, sin = rope_tables(max(wl.sq, wl.sk), wl.d)
+        cos = cos.to(dev) if cos is not None else None
+        sin = sin.to(dev) if sin is not None else None
+        out = torch.empty_like(q)
+        return lambda: ra.attention_forward_into(q, k, v, out, is_causal=wl.causal, window_size=wl.window,
+                                                 rot_cos=cos, rot_sin=sin)
+    if wl.kind == "int8":
+        qf = randn(wl.b, wl.hq, wl.sq, wl.d)
+        kf = randn(wl.b, wl.hkv, wl.sk, wl.d)
+        vf = randn(wl.b, wl.hkv, wl.sk, wl.d)
+        qi, ki, q_scale, k_scale = ra.quantize_int8_qk_pertoken(qf, kf)
+        _, _, vi, _, _, v_scale, _ = ra.quantize_int8_perchannel_v(qf, kf, vf)
+        del qf, kf, vf
+        out = torch.empty(qi.shape, dtype=torch.float16, device=dev)
+        return lambda: ra.attention_int8_forward_into(qi, ki, vi, out, q_scale, k_scale, v_scale,
+                                                      is_causal=wl.causal, window_size=wl.window)
+    if wl.kind == "decode":
+        # K/V are views of one [B, S, 2, Hkv, D] cache: head stride D, seq stride 2*Hkv*D
+        cache = randn(wl.b, wl.sk, 2, wl.hkv, wl.d).half()
+        k = cache[:, :, 0].transpose(1, 2)
+        v = cache[:, :, 1].transpose(1, 2)
+        q = randn(wl.b, wl.hq, wl.sq, wl.d).half()
+        out = torch.empty_like(q)
+        return lambda: ra.attention_forward_into(q, k, v, out, is_causal=wl.causal, window_size=wl.window)
+    raise ValueError(wl.kind)
+
+
+def time_steps(step, steps: int, warmup: int):
+    """Runs `warmup` untimed steps, then `steps` timed ones bracketed by
+    device synchronisation; returns (ms per step, mean kernel ms, launches, wall s)."""
+    import torch
+
+    import rdnattention_amd as ra
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    with ra.KernelTimer() as kt:
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(steps):
+            step()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    return start.elapsed_time(stop) / steps, kt.mean_ms, kt.launches, wall
+
+
+def roofline(wl: Workload, kernel_ms: float, traffic):
+    if wl.kind == "decode":
+        achieved = wl.io_bytes / (kernel_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    peak = INT8_PEAK_TOPS if wl.kind == "int8" else FP16_PEAK_TFLOPS
+    achieved = wl.flops / (kernel_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+            "unit": "TOP/s" if wl.kind == "int8" else "TFLOP/s", "frac": round(achieved / peak, 4),
+            "traffic": traffic}
+
+
+def profiled_traffic(name: str, wl: Workload):
+    """HBM bytes per launch of the workload's main kernel, from the committed
+    rocprofv3 counter summary profiles/<kernel>__<workload>.md (its
+    "traffic_bytes_per_launch:" line), or None when there is none."""
+    kern = re.sub(r"[<>]", "_", wl.kernel).strip("_")
+    path = ROOT / "profiles" / f"{kern}__{name}.md"
+    try:
+        text = path.read_text()
+    except OSError:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
+
+
+# --------------------------------------------------------------------------- #
+# CPU baselines
+# --------------------------------------------------------------------------- #
+def cpu_oracle_baseline(wl: Workload, host, budget_s: float = 12.0):
+    """The CPU oracle (oracle/attn_oracle.c: fp64 accumulation, threaded over
+    (batch, head, 64-row chunks)) on a bounded sample of the workload: the
+    first n (batch, kv head) units in batch-major order with their query
+    heads, full sequence, RoPE applied by the oracle first.  FLOPs counted
+    like the GPU's."""
+    import oracle
+
+    q, k, v, cos, sin = host
+    ratio = wl.hq // wl.hkv
+    units = wl.b * wl.hkv
+    threads = oracle.default_threads()
+    # flattening batch into heads keeps the GQA map: (b*Hq + h) / ratio = b*Hkv + h/ratio
+    qn = q.float().reshape(1, wl.b * wl.hq, wl.sq, wl.d).numpy()
+    kn = k.float().reshape(1, units, wl.sk, wl.d).numpy()
+    vn = v.float().reshape(1, units, wl.sk, wl.d).numpy()
+    cn = cos.numpy() if cos is not None else None
+    sn = sin.numpy() if sin is not None else None
+
+    def run(n):
+        qs, ks, vs = qn[:, : n * ratio], kn[:, :n], vn[:, :n]
+        t0 = time.perf_counter()
+        if wl.rope:
+            qs = oracle.rope(qs, cn, sn)
+            ks = oracle.rope(ks, cn, sn)
+        oracle.attention(qs, ks, vs, causal=wl.causal, window=wl.window, nthreads=threads)
+        return time.perf_counter() - t0
+
+    t1 = run(1)
+    n = max(1, min(units, int(budget_s / max(t1, 1e-6))))
+    t = run(n)
+    flops = attn_flops(1, n * ratio, wl.sq, wl.sk, wl.d, wl.causal, wl.window)
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"CPU oracle (C, fp64 accumulation, {threads} threads) on {cpu_model()} "
+                       f"(os.cpu_count()={os.cpu_count()}): {n} of {units} (batch, kv head) units = "
+                       f"{n * ratio} of {wl.b * wl.hq} query-head rows of S={wl.sq}, RoPE included, "
+                       f"one run of {t:.2f} s")}
+
+
+def cpu_sdpa_baseline(wl: Workload, host, budget_s: float = 12.0):
+    """torch CPU scaled_dot_product_attention (fp32, torch's default threads)
+    on a bounded sample: the first n (batch, kv head) units, full S."""
+    import torch
+
+    q, k, v, cos, sin = host
+    ratio = wl.hq // wl.hkv
+    units = wl.b * wl.hkv
+    delta = wl.sk - wl.sq
+    qf = q.reshape(1, wl.b * wl.hq, wl.sq, wl.d)
+    kf = k.reshape(1, units, wl.sk, wl.d)
+    vf = v.reshape(1, units, wl.sk, wl.d)
+
+    def run(n):
+        qs = qf[:, : n * ratio].float()
+        ks = kf[:, :n].float()
+        vs = vf[:, :n].float()
+        t0 = time.perf_counter()
+        if wl.rope:
             qs = rope_interleaved(qs, cos, sin)
             ks = rope_interleaved(ks, cos, sin)
         mask = None
         is_causal = False
-        if window > 0 or (causal and delta != 0):
-            i = torch.arange(sq)[:, None] + delta
-            j = torch.arange(sk)[None, :]
-            mask = torch.ones(sq, sk, dtype=torch.bool)
-            if causal:
+        if wl.window > 0 or (wl.causal and delta != 0):
+            i = torch.arange(wl.sq)[:, None] + delta
+            j = torch.arange(wl.sk)[None, :]
+            mask = torch.ones(wl.sq, wl.sk, dtype=torch.bool)
+            if wl.causal:
                 mask &= j <= i
-            if window > 0:
-                mask &= (i - j < window) if causal else ((i - j).abs() <= window // 2)
-        elif causal:
+            if wl.window > 0:
+                mask &= (i - j < wl.window) if wl.causal else ((i - j).abs() <= wl.window // 2)
+        elif wl.causal:
             is_causal = True
-        t0 = time.perf_counter()
         torch.nn.functional.scaled_dot_product_attention(qs, ks, vs, attn_mask=mask, is_causal=is_causal,
                                                          enable_gqa=ratio > 1)
         return time.perf_counter() - t0
 
-    run(1)  # warm-up (also sizes the sample)
-    t1 = min(run(1) for _ in range(2))
-    n_kv = max(1, min(hkv, int(budget_s / 3 / max(t1, 1e-6))))
-    times = sorted(run(n_kv) for _ in range(3))
-    t = times[1]
-    flops = attn_flops(1, n_kv * ratio, sq, sk, d, causal, window)
-    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": (f"torch.nn.functional.scaled_dot_product_attention fp32 on the host CPU "
-                       f"({cpu_model()}, os.cpu_count()={os.cpu_count()}), batch 1 of {b}, {n_kv * ratio} of {hq} "
-                       f"query heads, full S={sq}, median of 3 runs ({t:.2f} s); the reference has no CPU "
-                       f"attention path, so this is the CPU baseline its survey names")}
+    run(1)
+    t1 = run(1)
+    n = max(1, min(units, int(budget_s / 3 / max(t1, 1e-6))))
+    t = sorted(run(n) for _ in range(3))[1]
+    flops = attn_flops(1, n * ratio, wl.sq, wl.sk, wl.d, wl.causal, wl.window)
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "torch",
+            "sample": (f"torch.nn.functional.scaled_dot_product_attention fp32 on {cpu_model()}: {n} of {units} "
+                       f"(batch, kv head) units = {n * ratio} of {wl.b * wl.hq} query-head rows of S={wl.sq}, "
+                       f"RoPE with torch ops included, median of 3 runs ({t:.2f} s)")}
 
 
+# --------------------------------------------------------------------------- #
+# profiling helpers (run under rocprofv3 / on its output)
+# --------------------------------------------------------------------------- #
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(steps: int = 5) -> int:
+    """A plain device-to-device copy of COPY_BYTES (1 GiB read, 1 GiB written)
+    per launch, `steps` launches: under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    its per-dispatch KiB give the counters' scale against known traffic."""
+    import torch
+
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.float16, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": COPY_BYTES, "launches": steps}), flush=True)
+    return 0
+
+
+def pmc_summary(directory: str) -> int:
+    """Mean per-dispatch counter values per kernel from rocprofv3's
+    *counter_collection.csv files under `directory`."""
+    acc = {}
+    for path in sorted(Path(directory).rglob("*counter_collection.csv")):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                key = (row["Kernel_Name"], row["Counter_Name"])
+                s, n = acc.get(key, (0.0, 0))
+                acc[key] = (s + float(row["Counter_Value"]), n + 1)
+    if not acc:
+        print(f"no counter_collection.csv under {directory}", file=sys.stderr)
+        return 1
+    for (kern, ctr), (s, n) in sorted(acc.items()):
+        print(f"{ctr:<28} dispatches={n:<5} mean={s / n:16.1f}  {kern[:110]}")
+    return 0
+
+
+# --------------------------------------------------------------------------- #
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-secondary", action="store_true", help="measure the selected workload only")
+    ap.add_argument("--copy-calibration", action="store_true", help="run the 1 GiB copy used to scale counters")
+    ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 counter CSVs under DIR")
     args = ap.parse_args(argv)
+    if args.pmc_summary:
+        return pmc_summary(args.pmc_summary)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(attention shards by (batch, kv head) with no exchange); run with --gpus 1", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
 
     import torch
 
-    import rdnattention_amd
+    import rdnattention_amd as ra
 
-    spec = WORKLOADS[args.workload]
-    b, hq, hkv, sq, sk, d, causal, window, rope, seed, std = spec
     dev = torch.device("cuda:0")
-    q, k, v, cos, sin = make_inputs(spec)
-    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
-    cd = cos.to(dev) if cos is not None else None
-    sd = sin.to(dev) if sin is not None else None
-    out = torch.empty_like(qd)
-    flops = attn_flops(b, hq, sq, sk, d, causal, window)
+    name = args.workload
+    wl = WORKLOADS[name]
+    host = cpu_inputs(wl) if wl.kind == "f16" else None
+    step = make_step(wl, dev, host)
+    ms_step, kernel_ms, launches, wall = time_steps(step, args.steps, args.warmup)
+    del step
+    if launches != args.steps:
+        raise RuntimeError(f"kernel timer saw {launches} launches for {args.steps} steps")
+    if wl.kind == "decode":
+        value, unit = wl.io_bytes / (ms_step * 1e-3) / 1e9, "GB/s"
+    else:
+        value, unit = wl.flops / (ms_step * 1e-3) / 1e12, ("TOP/s" if wl.kind == "int8" else "TFLOP/s")
 
-    def step():
-        rdnattention_amd.attention_forward_into(qd, kd, vd, out, is_causal=causal, window_size=window, rot_cos=cd,
-                                                rot_sin=sd)
+    secondary = {}
+    if not args.no_secondary and name == DEFAULT:
+        for other in SECONDARY:
+            owl = WORKLOADS[other]
+            try:
+                ostep = make_step(owl, dev)
+                oms, okms, _, _ = time_steps(ostep, 10, 3)
+                del ostep
+                rf = roofline(owl, okms, profiled_traffic(other, owl))
+                secondary[other] = {"ms_per_step": round(oms, 4), "kernel_ms": round(okms, 4), "roofline": rf}
+            except ra.RDNAttentionError as e:
+                secondary[other] = {"error": str(e)}
+            torch.cuda.empty_cache()
+        i8 = secondary.get("int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128", {})
+        f16 = secondary.get("fp16_causal_gqa_b2_h32_kv8_s8192_d128", {})
+        if "kernel_ms" in i8 and "kernel_ms" in f16:
+            secondary["int8_over_fp16_same_shape"] = round(f16["kernel_ms"] / i8["kernel_ms"], 3)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    t0 = time.perf_counter()
-    ev[0].record(stream)
-    for i in range(args.steps):
-        step()
-        ev[i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_launch_ms = [ev[i].elapsed_time(ev[i + 1]) for i in range(args.steps)]
-    ms_total = ev[0].elapsed_time(ev[-1])
-    ms_step = ms_total / args.steps
-    tflops = flops / (ms_step * 1e-3) / 1e12
-    per_launch_ms.sort()
-    med_ms = per_launch_ms[len(per_launch_ms) // 2]
-    achieved = flops / (sum(per_launch_ms) / len(per_launch_ms) * 1e-3) / 1e12
+    cpu = sdpa = None
+    if not args.no_cpu and host is not None:
+        cpu = cpu_oracle_baseline(wl, host)
+        sdpa = cpu_sdpa_baseline(wl, host)
 
-    cpu = None if args.no_cpu else cpu_baseline(spec, q, k, v, cos, sin)
     line = {
         "metric": METRIC,
-        "value": round(tflops, 2),
-        "unit": "TFLOP/s",
+        "value": round(value, 2),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -220,15 +488,18 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic N(0,1) fp16 from CPU torch.Generator(seed), resident in HBM",
-        "config": {"workload": args.workload, "batch": b, "num_heads": hq, "num_kv_heads": hkv, "seq_len": sq,
-                   "key_seq_len": sk, "head_dim": d, "causal": causal, "window_size": window, "rope": rope,
-                   "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4), "traffic": None},
+        "dtype": {"f16": "fp16", "int8": "int8", "decode": "fp16"}[wl.kind],
+        "data": ("synthetic N(0,%g) from torch.Generator(seed=%d), resident in HBM" % (wl.std, wl.seed)),
+        "config": {"workload": name, "batch": wl.b, "num_heads": wl.hq, "num_kv_heads": wl.hkv,
+                   "seq_len": wl.sq, "key_seq_len": wl.sk, "head_dim": wl.d, "causal": wl.causal,
+                   "window_size": wl.window, "rope": wl.rope, "parallelism": "single GPU"},
+        "roofline": roofline(wl, kernel_ms, profiled_traffic(name, wl)),
         "cpu_baseline": cpu,
-        "kernel_ms_median": round(med_ms, 4),
+        "cpu_sdpa": sdpa,
+        "kernel": wl.kernel,
+        "kernel_ms_mean": round(kernel_ms, 4),
+        "algorithmic_bytes_per_launch": wl.io_bytes,
+        "secondary": secondary or None,
         "wall_s": round(wall, 3),
     }
     print(json.dumps(line), flush=True)

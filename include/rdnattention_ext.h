@@ -42,6 +42,18 @@ RDNA_API int32_t rdna_int8_qk_scores(
     uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
     void* hip_stream);
 
+/* Kernel timer.  While enabled, each launch of a main attention kernel
+ * (prefill, split-K, int8; not the RoPE pre-rotation or split-K combine
+ * kernels) is bracketed by a HIP event pair recorded on its stream.
+ * rdna_kernel_timer_enable(on) discards what was recorded and switches the
+ * timer on (on != 0) or off.  rdna_kernel_timer_read waits for the recorded
+ * events, stores the summed kernel time in *total_ms and the number of timed
+ * launches in *launches, and clears the record; returns -3 if an event could
+ * not be created, recorded or read.  Process-wide; no reference counterpart:
+ * benchmarks use it to divide a kernel's FLOPs or bytes by its own time. */
+RDNA_API int32_t rdna_kernel_timer_enable(int32_t on);
+RDNA_API int32_t rdna_kernel_timer_read(double* total_ms, int64_t* launches);
+
 /* Library version string ("0.1.0-gfx950"). */
 RDNA_API const char* rdna_version(void);
 

@@ -88,6 +88,10 @@ def _lib_handle():
         lib.rdna_attention_forward_int8qk.restype = _I32
         lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
         lib.rdna_int8_qk_scores.restype = _I32
+        lib.rdna_kernel_timer_enable.argtypes = [_I32]
+        lib.rdna_kernel_timer_enable.restype = _I32
+        lib.rdna_kernel_timer_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]
+        lib.rdna_kernel_timer_read.restype = _I32
         lib.rdna_version.argtypes = []
         lib.rdna_version.restype = ctypes.c_char_p
         _lib = lib
@@ -288,6 +292,78 @@ def flash_attn_int8qk(query, key, value, q_scale, k_scale, v_scale: float, is_ca
     if result != 0:
         raise RDNAttentionError(f"flash_attn_int8qk failed: {last_error()}")
     return output
+
+
+def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_scale: float, *,
+                                is_causal: bool = False, window_size: int = -1, scale=None) -> None:
+    """INT8 forward written into a preallocated float16 `output` (the raw
+    rdna_attention_forward_int8qk call, src/c_api.cpp:116-195).
+
+    query/key/value: int8 [batch, heads, seq, head_dim] views with a
+    contiguous head_dim axis and batch/head/seq strides that are multiples of
+    16 elements.  q_scale/k_scale: floats, or contiguous float32 device
+    tensors of per-token scales [batch, heads, seq_len] /
+    [batch, kv_heads, key_seq_len].  Asynchronous on torch's current stream."""
+    import torch
+
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.int8 or t.dim() != 4 or not t.is_cuda:
+            raise ValueError(f"{name} must be a 4D int8 HIP tensor")
+    if output.dtype != torch.float16 or output.shape != query.shape or not output.is_cuda:
+        raise ValueError("output must be a float16 HIP tensor with the shape of query")
+    batch, heads, seq_len, head_dim = query.shape
+    _, kv_heads, key_seq_len, _ = key.shape
+
+    def _scale_arg(x, name, want):
+        if not isinstance(x, torch.Tensor):
+            return float(x), None
+        if x.dtype != torch.float32 or not x.is_contiguous() or tuple(x.shape) != want or not x.is_cuda:
+            raise ValueError(f"{name} must be a contiguous float32 HIP tensor of shape {want}")
+        return 1.0, x
+
+    q_scalar, q_vec = _scale_arg(q_scale, "q_scale", (batch, heads, seq_len))
+    k_scalar, k_vec = _scale_arg(k_scale, "k_scale", (batch, kv_heads, key_seq_len))
+    qs, ks, vs, os_ = query.stride(), key.stride(), value.stride(), output.stride()
+    result = _lib_handle().rdna_attention_forward_int8qk(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
+        batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
+        float(head_dim ** -0.5 if scale is None else scale), q_scalar, k_scalar, float(v_scale),
+        q_vec.data_ptr() if q_vec is not None else None, k_vec.data_ptr() if k_vec is not None else None,
+        1 if is_causal else 0, int(window_size), _stream())
+    if result != 0:
+        raise RDNAttentionError(f"attention_int8_forward_into failed: {last_error()}")
+
+
+class KernelTimer:
+    """Context manager timing the library's main attention kernels with HIP
+    events recorded on their launch streams (rdna_kernel_timer_enable/_read):
+    RoPE pre-rotation and split-K combine launches are not included.  After
+    the block, `total_ms` and `launches` hold the summed kernel time and the
+    number of timed launches; `mean_ms` their ratio."""
+
+    def __init__(self):
+        self.total_ms = 0.0
+        self.launches = 0
+
+    @property
+    def mean_ms(self) -> float:
+        return self.total_ms / self.launches if self.launches else float("nan")
+
+    def __enter__(self):
+        _lib_handle().rdna_kernel_timer_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib = _lib_handle()
+        ms = ctypes.c_double(0.0)
+        n = _I64(0)
+        rc = lib.rdna_kernel_timer_read(ctypes.byref(ms), ctypes.byref(n))
+        lib.rdna_kernel_timer_enable(0)
+        if rc != 0 and exc[0] is None:
+            raise RDNAttentionError("kernel timer: a HIP event could not be created, recorded or read")
+        self.total_ms, self.launches = ms.value, n.value
+        return False
 
 
 def quantize_int8_perchannel_v(query, key, value):

@@ -390,6 +390,7 @@ __global__ __launch_bounds__(128) void fa_decode_combine(CombineParams p) {
 
 template <int D>
 int launch_decode(const DecodeParams& p, int n_bkv, hipStream_t stream, std::string& err) {
+    KernelTimerGuard timer(stream);
     hipLaunchKernelGGL(fa_fwd_f16_decode<D>, dim3(p.splits, n_bkv), dim3(kDecThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

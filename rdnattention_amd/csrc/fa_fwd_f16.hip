@@ -704,6 +704,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
 
 template <int D>
 int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    KernelTimerGuard timer(stream);
     hipLaunchKernelGGL(fa_fwd_f16_pp<D>, dim3((uint32_t)n_wg), dim3(kPPThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -715,6 +716,7 @@ int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::str
 
 template <int D>
 int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    KernelTimerGuard timer(stream);
     hipLaunchKernelGGL(fa_fwd_f16_prefill<D>, dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

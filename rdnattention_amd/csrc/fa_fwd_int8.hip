@@ -429,6 +429,7 @@ __global__ __launch_bounds__(64) void int8_scores_kernel(const int8_t* __restric
 
 template <int D>
 int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    KernelTimerGuard timer(stream);
     hipLaunchKernelGGL(fa_fwd_int8<D>, dim3((uint32_t)n_wg), dim3(kI8Threads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

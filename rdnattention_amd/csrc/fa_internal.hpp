@@ -28,6 +28,22 @@ struct StreamScratch {
 // [B, Hkv, Sk, D], with the tables a.rot_cos / a.rot_sin.
 int rope_rotate_k(const AttnArgs& a, void* dst, hipStream_t stream, std::string& err);
 
+// Kernel timer for measurement.  While enabled (rdna_kernel_timer_enable),
+// every launch of a main attention kernel is bracketed by a HIP event pair
+// recorded on the launch stream; rdna_kernel_timer_read sums the elapsed
+// times.  Disabled, the guard costs one relaxed atomic load.
+class KernelTimerGuard {
+  public:
+    explicit KernelTimerGuard(hipStream_t stream);
+    ~KernelTimerGuard();
+    KernelTimerGuard(const KernelTimerGuard&) = delete;
+    KernelTimerGuard& operator=(const KernelTimerGuard&) = delete;
+
+  private:
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+};
+
 // Launchers.
 int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err);
 int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err);

@@ -184,3 +184,18 @@ def test_python_missing_library(monkeypatch, tmp_path):
     monkeypatch.setattr(ra, "_lib", None)
     with pytest.raises(ra.RDNAttentionError, match="missing file"):
         ra.has_device()
+
+
+def test_kernel_timer_without_launches(lib):
+    """Enable/read of the kernel timer with nothing launched: no HIP call is
+    made, zero launches are reported, the record is cleared."""
+    import ctypes
+
+    lib.rdna_kernel_timer_enable.argtypes = [ctypes.c_int32]
+    lib.rdna_kernel_timer_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64)]
+    assert lib.rdna_kernel_timer_enable(1) == 0
+    ms, n = ctypes.c_double(-1.0), ctypes.c_int64(-1)
+    assert lib.rdna_kernel_timer_read(ctypes.byref(ms), ctypes.byref(n)) == 0
+    assert ms.value == 0.0 and n.value == 0
+    assert lib.rdna_kernel_timer_read(None, None) == -3
+    assert lib.rdna_kernel_timer_enable(0) == 0

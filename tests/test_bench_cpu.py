@@ -32,13 +32,49 @@ def test_rope_interleaved_matches_oracle(oracle_lib):
     np.testing.assert_allclose(got.numpy(), ref, atol=1e-6)
 
 
-def test_cpu_baseline_small():
+def test_cpu_baselines_small(oracle_lib):
     import bench
 
-    spec = (1, 4, 2, 256, 256, 64, True, -1, True, 0, 1.0)
-    q, k, v, cos, sin = bench.make_inputs(spec)
-    r = bench.cpu_baseline(spec, q, k, v, cos, sin, budget_s=0.5)
+    wl = bench.Workload("f16", 1, 4, 2, 256, 256, 64, True, -1, True, 0, 1.0, "fa_fwd_f16_pp<64>")
+    host = bench.cpu_inputs(wl)
+    r = bench.cpu_oracle_baseline(wl, host, budget_s=0.5)
     assert r["value"] > 0 and r["cores"] >= 1 and r["kind"] == "port"
+    r = bench.cpu_sdpa_baseline(wl, host, budget_s=0.5)
+    assert r["value"] > 0 and r["cores"] >= 1
+
+
+def test_io_bytes_and_flops():
+    import bench
+
+    wl = bench.WORKLOADS["fp16_decode_b16_h32_kv8_sq1_sk32768_d128"]
+    # Q + O (16*32*1*128 fp16 each) + K + V (16*8*32768*128 fp16 each)
+    assert wl.io_bytes == 2 * 16 * 32 * 128 * 2 + 2 * 16 * 8 * 32768 * 128 * 2
+    head = bench.WORKLOADS[bench.DEFAULT]
+    assert head.flops == 4 * 4 * 32 * (4096 * 4097 // 2) * 128
+
+
+def test_profiled_traffic_parses(tmp_path, monkeypatch):
+    import bench
+
+    wl = bench.WORKLOADS[bench.DEFAULT]
+    monkeypatch.setattr(bench, "ROOT", tmp_path)
+    assert bench.profiled_traffic(bench.DEFAULT, wl) is None
+    (tmp_path / "profiles").mkdir()
+    (tmp_path / "profiles" / f"fa_fwd_f16_pp_128__{bench.DEFAULT}.md").write_text(
+        "# x\n\ntraffic_bytes_per_launch: 123456\n")
+    assert bench.profiled_traffic(bench.DEFAULT, wl) == 123456
+
+
+def test_pmc_summary(tmp_path, capsys):
+    import bench
+
+    d = tmp_path / "run"
+    d.mkdir()
+    (d / "run_counter_collection.csv").write_text(
+        '"Kernel_Name","Counter_Name","Counter_Value"\n"k1","FETCH_SIZE",10.0\n"k1","FETCH_SIZE",30.0\n')
+    assert bench.pmc_summary(str(tmp_path)) == 0
+    out = capsys.readouterr().out
+    assert "FETCH_SIZE" in out and "dispatches=2" in out and "20.0" in out
 
 
 def test_multi_gpu_refused():
