@@ -25,6 +25,7 @@
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
+#include "fa_prefill.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -32,29 +33,6 @@
 
 namespace rdna_amd {
 namespace {
-
-struct PrefillParams {
-    const _Float16* q;
-    const _Float16* k;
-    const _Float16* v;
-    _Float16* o;
-    const float* rot_cos;
-    const float* rot_sin;
-    int64_t q_sb, q_sh, q_ss;
-    int64_t k_sb, k_sh, k_ss;
-    int64_t v_sb, v_sh, v_ss;
-    int64_t o_sb, o_sh, o_ss;
-    int32_t Sq, Hkv, ratio;
-    int32_t G;             // query heads per workgroup
-    int32_t rows_per_wg;   // query rows per head per workgroup (128 / G)
-    int32_t n_row_tiles;   // ceil(Sq / rows_per_wg)
-    int32_t n_head_groups; // B * Hkv * groups_per_kv
-    int32_t groups_per_kv; // ratio / G
-    float c;               // max(|scale| * log2(e), 1e-30)
-    float q_sign;          // sign of scale, folded into Q (exact in fp16)
-    MaskSpec mask;
-    int32_t rope_q;        // rotate Q with rot_cos / rot_sin while loading it
-};
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -787,6 +765,9 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     case 224: return launch_prefill<224>(p, n_wg, stream, err);
     case 256: return launch_prefill<256>(p, n_wg, stream, err);
     default: break;
+    }
+    if (a.D > 256) {
+        return launch_wide(p, (int)a.D, n_wg, stream, err);
     }
     err = "unsupported head_dim (multiples of 32 from 32 to 512)";
     return -1;

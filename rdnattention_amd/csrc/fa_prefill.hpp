@@ -1,0 +1,39 @@
+// Parameter block of the FP16 prefill kernels (device-side headers only).
+#pragma once
+
+#include "fa_common.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+namespace rdna_amd {
+
+struct PrefillParams {
+    const _Float16* q;
+    const _Float16* k;
+    const _Float16* v;
+    _Float16* o;
+    const float* rot_cos;
+    const float* rot_sin;
+    int64_t q_sb, q_sh, q_ss;
+    int64_t k_sb, k_sh, k_ss;
+    int64_t v_sb, v_sh, v_ss;
+    int64_t o_sb, o_sh, o_ss;
+    int32_t Sq, Hkv, ratio;
+    int32_t G;             // query heads per workgroup
+    int32_t rows_per_wg;   // query rows per head per workgroup (32 * waves / G)
+    int32_t n_row_tiles;   // ceil(Sq / rows_per_wg)
+    int32_t n_head_groups; // B * Hkv * groups_per_kv
+    int32_t groups_per_kv; // ratio / G
+    float c;               // max(|scale| * log2(e), 1e-30)
+    float q_sign;          // sign of scale, folded into Q (exact in fp16)
+    MaskSpec mask;
+    int32_t rope_q;        // rotate Q with rot_cos / rot_sin while loading it
+};
+
+// Large-head prefill (head_dim 288..512 in steps of 32), fa_fwd_f16_wide.hip.
+int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
+
+} // namespace rdna_amd

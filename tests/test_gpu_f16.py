@@ -17,8 +17,6 @@ from tests.gpu_util import (assert_f16_parity, forward_raw, gate_rope_tables, lc
 
 pytestmark = pytest.mark.gpu
 
-LARGE_D_PENDING = 256  # head dims above this use the large-head kernel
-
 # name, batch, numHeads, numKvHeads, seqLen, keySeqLen, headDim, causal, windowSize, hasRope
 GATE_CASES = [
     ("d64_dense_small", 1, 4, 4, 96, 96, 64, False, 0, False),
@@ -74,15 +72,9 @@ GATE_CASES = [
 ]
 
 
-def _skip_large(d):
-    if d > LARGE_D_PENDING:
-        pytest.skip("head_dim > 256: large-head kernel not built yet")
-
-
 @pytest.mark.parametrize("case", GATE_CASES, ids=[c[0] for c in GATE_CASES])
 def test_gate_cases(gpu, oracle_lib, case):
     name, b, hq, hkv, sq, sk, d, causal, window, rope = case
-    _skip_large(d)
     log(f"[gate] {name}")
     q, k, v = lcg_inputs(12345, b, hq, hkv, sq, sk, d, mode=0)
     cos = sin = None
@@ -118,7 +110,6 @@ def test_head_dim_python_path(gpu, oracle_lib, d, variant):
     """tests/head_dim.py through rdnattention_amd.flash_attn (8 heads, N(0,1))."""
     import rdnattention_amd
 
-    _skip_large(d)
     name, kvdiv, s_len, ks_len, causal, window = variant
     torch.manual_seed(1234)
     h = 8
@@ -223,8 +214,9 @@ def test_rows_without_keys_are_zero(gpu, oracle_lib):
     assert_f16_parity(o, reference_f16(q, k, v, True, -1), "no_keys")
 
 
-def test_first_causal_row_exact(gpu):
-    q, k, v = seeded_inputs(6, 1, 4, 4, 128, 128, 128)
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_first_causal_row_exact(gpu, d):
+    q, k, v = seeded_inputs(6, 1, 4, 4, 128, 128, d)
     out = torch.empty_like(q, device=gpu)
     assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal=True) == 0
     torch.cuda.synchronize()
@@ -249,3 +241,37 @@ def test_empty_key_sequence_outputs_zero(gpu):
     assert forward_raw(q, k, k, out) == 0
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("d,s,window", [(256, 2048, 1024), (512, 1024, 1024), (416, 640, 256)])
+def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
+    """The large-head window workloads (two-sided window, RoPE, N(0, 0.5)) at
+    a size the oracle finishes quickly; D = 416 runs the two overlapping
+    column passes."""
+    q, k, v = seeded_inputs(4, 1, 2, 2, s, s, d, std=0.5)
+    cos, sin = oracle.rope_tables(s, d)
+    out = torch.empty_like(q, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, False, window, torch.from_numpy(cos).to(gpu),
+                       torch.from_numpy(sin).to(gpu)) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, False, window, cos, sin)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_window{window}")
+
+
+@pytest.mark.parametrize("d", [288, 512])
+def test_large_head_strided_kv_bit_identical(gpu, oracle_lib, d):
+    """Large-head kernel with K/V sliced from one [B,S,2,Hkv,D] buffer."""
+    g = torch.Generator().manual_seed(9)
+    b, hq, hkv, sq, sk = 1, 4, 2, 70, 133
+    buf = torch.randn(b, sk, 2, hkv, d, generator=g).half().to(gpu)
+    q = torch.randn(b, hq, sq, d, generator=g).half().to(gpu)
+    kv_k = buf[:, :, 0].transpose(1, 2)
+    kv_v = buf[:, :, 1].transpose(1, 2)
+    o1 = torch.empty_like(q)
+    o2 = torch.empty_like(q)
+    assert forward_raw(q, kv_k, kv_v, o1, causal=True) == 0
+    assert forward_raw(q, kv_k.contiguous(), kv_v.contiguous(), o2, causal=True) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert_f16_parity(o1.float().cpu().numpy(), reference_f16(q.cpu(), kv_k.cpu(), kv_v.cpu(), True, -1),
+                      f"strided_d{d}")
