@@ -1,5 +1,6 @@
-// INT8 FlashAttention forward for gfx950: both GEMMs on int8 MFMA
-// (v_mfma_i32_32x32x32_i8, exact int32 accumulation), fp16 output.
+// INT8 FlashAttention forward for gfx950: Q K^T on int8 MFMA
+// (v_mfma_i32_32x32x32_i8, exact int32 accumulation), P V on fp16 MFMA with
+// integer operands (exact), fp16 output.
 //
 // Replaces the reference's forwardKernelInt8QK
 // (src/rdna/fa2_forward_int8qk.hip:229-495) and keeps its numeric scheme:
@@ -9,20 +10,23 @@
 //   per 64-key block, aligned to key 0 (the reference's Bc = 64):
 //     m'  = max(m, max_j s_ij);  O *= 2^(m - m'),  l *= 2^(m - m')
 //     p   = 2^(s - m'),  l += sum p                  (unquantised p)
-//     pq  = min(127, round(p * 127))                 (int8 P)
-//     O  += (float)(sum_j pq_j v_j) * (v_scale / 127) (exact int32 GEMM)
-//   out = O / l  (0 when no key is visible)
+//     pq  = min(127, round(p * 127))                 (P as integers 0..127)
+//     O  += sum_j pq_j v_j                           (exact integer products)
+//   out = O * v_scale / (127 l)  (0 when no key is visible)
 //
-// The one deliberate difference: round() here is round-half-to-even
-// (v_rndne_f32) where the reference calls lroundf (half away from zero); they
-// differ only when p * 127 is exactly k + 0.5.
+// Deliberate differences, all below the INT8 tolerance: round() is
+// round-half-to-even (v_rndne_f32) where the reference calls lroundf (half
+// away from zero), 127 p is evaluated as 2^(s - m' + log2 127), and the per-
+// block v_scale/127 factor is applied once at the end.  pq * v products are
+// exact in fp16 MFMA (|pq| <= 127, |v| <= 127) and a block's sums stay below
+// 2^24, so P V on fp16 MFMA gives the same integers as the reference's int32
+// GEMM while O accumulates in fp32 without a per-block conversion pass.
 //
 // Kernel structure is the FP16 ping-pong design (fa_fwd_f16.hip): 8 waves in
 // two groups alternating MFMA and VALU phases, S^T = K Q^T so a lane owns one
-// query column, P^T going from the S accumulator straight into the B operand
-// of O^T = V^T P^T, and V^T read with the byte transpose read
-// ds_read_b64_tr_b8 (in each 16-lane group, lane i's byte k is byte i % 8 of
-// the 8-byte word addressed by lane 2k + i/8).
+// query column, and P^T going from the S accumulator straight into the B
+// operand of O^T = V^T P^T.  V is converted to fp16 while it is staged into
+// LDS and its V^T operands come from ds_read_b64_tr_b16 transpose reads.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
@@ -52,7 +56,7 @@ struct Int8Params {
     const float* qsv; // [B, Hq, Sq] or null
     const float* ksv; // [B, Hkv, Sk] or null
     float q_scale, k_scale;
-    float pv_scale; // v_scale / 127
+    float v_scale;
     float scale_log2e;
     int64_t q_sb, q_sh, q_ss;
     int64_t k_sb, k_sh, k_ss;
@@ -64,21 +68,22 @@ struct Int8Params {
 
 template <int D>
 struct I8Cfg {
-    static constexpr int LD = D + 16; // LDS row stride in bytes (16 B step mod 256 across rows)
-    static constexpr int TILE = kI8BN * LD;
-    static constexpr int NS = D / 32;  // QK^T reduction steps (32 int8 per MFMA)
-    static constexpr int NDT = D / 32; // O^T row tiles
-    static constexpr int KCH = D / 16; // 16-byte chunks per row
-    static constexpr int HALF_TASK = 32 * KCH;
+    // K: int8 rows of D bytes at a D+16 byte stride (16 rows read with
+    // ds_read_b128 land in distinct banks); V: converted to fp16 while staged,
+    // rows at D+32 halves (conflict-free 4-row transpose reads)
+    static constexpr int LDK = D + 16;         // bytes
+    static constexpr int LDV = D + 32;         // halves
+    static constexpr int TILE_K = kI8BN * LDK; // bytes
+    static constexpr int TILE_V = kI8BN * LDV; // halves
+    static constexpr int NS = D / 32;          // int8 QK^T reduction steps (32 per MFMA)
+    static constexpr int NDT = D / 32;         // O^T row tiles
+    static constexpr int KCH = D / 16;         // 16-byte int8 chunks per row
+    static constexpr int HALF_TASK = 32 * KCH; // one group's chunks of one K (or V) tile
     static constexpr int CT = (HALF_TASK + 255) / 256;
 };
 
-__device__ __forceinline__ i2 lds_read_tr8(const int8_t* p) {
-    typedef __attribute__((address_space(3))) i2 lds_i2;
-    const auto* lp = reinterpret_cast<const __attribute__((address_space(3))) char*>(
-        (uint32_t)reinterpret_cast<uintptr_t>(p));
-    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i2*)lp);
-}
+constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
+constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
 
 __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -86,19 +91,34 @@ __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(i4, x);
 }
 
-// p in [0, 1] -> round(p * 127) as a byte, packed into byte `sel` of `old`
-__device__ __forceinline__ uint32_t quant_p(float p, uint32_t old, int sel) {
-    float y = fminf(__builtin_rintf(p * 127.0f), 127.0f);
-    return __builtin_amdgcn_cvt_pk_u8_f32(y, sel, old);
+// 16 signed bytes -> two h8 (exact: every int8 is an fp16 integer)
+__device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
+    const i8x8 a = __builtin_bit_cast(i8x8, i2{w[0], w[1]});
+    const i8x8 b = __builtin_bit_cast(i8x8, i2{w[2], w[3]});
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        lo[e] = (_Float16)a[e];
+        hi[e] = (_Float16)b[e];
+    }
 }
 
+// Scheme (the reference's, fa2_forward_int8qk.hip:281-382), per 64-key block b
+// aligned to key 0, with s_j = S_j * qs * ks_j * scale * log2(e):
+//   m_b  = max(m_{b-1}, max_j s_j),  corr = 2^(m_{b-1} - m_b)
+//   y_j  = 127 * 2^(s_j - m_b)         (computed as 2^(s_j - m_b + log2 127))
+//   pq_j = round(y_j) in [0, 127]      (P: exact integers in fp16)
+//   l    = l * corr + sum_j y_j        (unquantised p, in units of 1/127)
+//   O    = O * corr + sum_j pq_j v_j   (exact integer products, fp32 sums)
+//   out  = O * v_scale / l
+// S runs on int8 MFMA (exact int32).  P V runs on fp16 MFMA, which is exact
+// for these integer operands and accumulates straight into fp32, so O needs
+// no per-block int32 -> fp32 conversion.
 template <int D>
 __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     using C = I8Cfg<D>;
-    __shared__ __attribute__((aligned(16))) int8_t smem[4 * C::TILE];
+    __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
+    __shared__ __attribute__((aligned(16))) _Float16 sVs[2 * C::TILE_V];
     __shared__ __attribute__((aligned(16))) float sks[2][kI8BN];
-    int8_t* const sKs = smem;
-    int8_t* const sVs = smem + 2 * C::TILE;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -144,7 +164,12 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             qs = p.qsv[((int64_t)b * p.Hq + h) * p.Sq + q];
         }
     }
+    // s_j = t_j * qc with t_j = S_j * ks_j.  When every lane's qc is positive
+    // the row max is taken over t (one multiply per score saved); otherwise t
+    // is first scaled by qc in place and qeff = 1.
     const float qc = qs * p.scale_log2e;
+    const bool qpos = !wave_any(!(qc > 0.0f));
+    const float qeff = qpos ? qc : 1.0f;
 
     const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
     int klo, khi;
@@ -163,16 +188,20 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         oacc[dt] = f16x{};
     }
     float m_run = -INFINITY, l_run = 0.0f;
-    f16x sf[2]; // scores of the current tile, fp32, log2 domain
-    sf[0] = f16x{};
-    sf[1] = f16x{};
-    i4 pb[2] = {i4{}, i4{}};
+    i16x sacc[2]; // int32 scores of the current tile
+    sacc[0] = i16x{};
+    sacc[1] = i16x{};
+    h8 pb[4]; // P^T operands of the four 16-key groups: integers 0..127 in fp16
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        pb[u] = h8{};
+    }
     int cls_prev = 0;
 
     // ---- staging (one group's 32 rows of K and V per pair; ks by group A)
     i4 kreg[C::CT], vreg[C::CT];
     uint32_t coff_k[C::CT], coff_v[C::CT];
-    int cl[C::CT];
+    int clk[C::CT], clv[C::CT];
 #pragma unroll
     for (int it = 0; it < C::CT; it++) {
         const int e = gtid + it * 256;
@@ -181,7 +210,8 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
         coff_k[it] = (uint32_t)((int64_t)row * p.k_ss + 16 * ch);
         coff_v[it] = (uint32_t)((int64_t)row * p.v_ss + 16 * ch);
-        cl[it] = ok ? row * C::LD + 16 * ch : -1;
+        clk[it] = ok ? row * C::LDK + 16 * ch : -1;
+        clv[it] = ok ? row * C::LDV + 16 * ch : -1;
     }
     float ksreg = 0.0f;
     auto load_pair = [&](int x) {
@@ -201,16 +231,19 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         }
     };
     auto store_pair = [&](int x) {
-        int8_t* sK = sKs + (x & 1) * C::TILE;
-        int8_t* sV = sVs + ((x - 1) & 1) * C::TILE;
+        int8_t* sK = sKs + (x & 1) * C::TILE_K;
+        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
 #pragma unroll
         for (int it = 0; it < C::CT; it++) {
-            if (C::HALF_TASK % 256 == 0 || cl[it] >= 0) {
+            if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
                 if (x < n) {
-                    *reinterpret_cast<i4*>(&sK[cl[it]]) = kreg[it];
+                    *reinterpret_cast<i4*>(&sK[clk[it]]) = kreg[it];
                 }
                 if (x >= 1 && x <= n) {
-                    *reinterpret_cast<i4*>(&sV[cl[it]]) = vreg[it];
+                    h8 lo, hi;
+                    i8x16_to_h8x2(vreg[it], lo, hi);
+                    *reinterpret_cast<h8*>(&sV[clv[it]]) = lo;
+                    *reinterpret_cast<h8*>(&sV[clv[it] + 8]) = hi;
                 }
             }
         }
@@ -219,73 +252,110 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         }
     };
 
-    // M(i): O += V(i-1)^T P(i-1) (int32, converted per block) and S(i) = K(i) Q^T
+    // M(i): O^T += V(i-1)^T P(i-1)^T (fp16 MFMA, i >= 1) then S(i)^T = K(i) Q^T
+    // (int8 MFMA, i < n): one stream of MFMAs whose LDS operands are read
+    // kI8OpDepth MFMAs ahead through a register ring
+    auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+        constexpr bool DO_PV = decltype(do_pv_c)::value;
+        constexpr bool DO_S = decltype(do_s_c)::value;
+        constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
+        constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
+        constexpr int T = NPV + NSK;
+        constexpr int DEPTH = T < kI8OpDepth ? T : kI8OpDepth;
+        const int j16 = lane & 15;
+        const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
+                               16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+        const int8_t* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 16 * g;
+        auto op = [&](int j) -> i4 {
+            if (j < NPV) {
+                const int u = j / C::NDT, dt = j % C::NDT;
+                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+            const int js = j - NPV, st = js >> 1, kt = js & 1;
+            return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
+        };
+        i16x acc0 = {}, acc1 = {};
+        i4 ring[DEPTH > 0 ? DEPTH : 1];
+#pragma unroll
+        for (int j = 0; j < DEPTH; j++) {
+            ring[j] = op(j);
+        }
+#pragma unroll
+        for (int j = 0; j < T; j++) {
+            const i4 a = ring[j % DEPTH];
+            if (j + DEPTH < T) {
+                ring[j % DEPTH] = op(j + DEPTH);
+            }
+            if (j < NPV) {
+                const int u = j / C::NDT, dt = j % C::NDT;
+                oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
+            } else {
+                const int js = j - NPV, st = js >> 1;
+                if (js & 1) {
+                    acc1 = mfma_32x32x32_i8(a, qreg[st], acc1);
+                } else {
+                    acc0 = mfma_32x32x32_i8(a, qreg[st], acc0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (DO_S) {
+            sacc[0] = acc0;
+            sacc[1] = acc1;
+        }
+    };
     auto phase_m = [&](int i) {
         if (!wave_active) {
             return;
         }
+        const bool do_pv = i >= 1 && cls_prev != 0;
         int cls_now = 0;
         if (i < n) {
             const int kt0 = (t_begin + i) * kI8BN;
             cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kI8BN - 1);
         }
-        if (i >= 1 && cls_prev != 0) {
-            const int8_t* sV = sVs + ((i - 1) & 1) * C::TILE;
-            // lane j of each 16-lane group points at key row kr(j/2), bytes
-            // 8*(j%2) of the group's 16-column half of the d tile
-            const int j16 = lane & 15;
-            const int dcol = 16 * ((lane >> 4) & 1) + 8 * (j16 & 1);
-            const int kk = j16 >> 1; // slot 0..7 of this read
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-                i16x acc = {};
-#pragma unroll
-                for (int kt = 0; kt < 2; kt++) {
-                    i2 part[2];
-#pragma unroll
-                    for (int hh = 0; hh < 2; hh++) {
-                        const int slot = 8 * hh + kk; // key = 8*(slot/4) + 4g + slot%4
-                        const int row = 32 * kt + 8 * (slot >> 2) + 4 * g + (slot & 3);
-                        part[hh] = lds_read_tr8(sV + row * C::LD + 32 * dt + dcol);
-                    }
-                    i4 a = {part[0][0], part[0][1], part[1][0], part[1][1]};
-                    acc = mfma_32x32x32_i8(a, pb[kt], acc);
-                }
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    oacc[dt][e] = fmaf((float)acc[e], p.pv_scale, oacc[dt][e]);
-                }
-            }
-        }
-        if (cls_now != 0) {
-            const int8_t* sK = sKs + (i & 1) * C::TILE;
-            const float* ksl = sks[i & 1];
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                i16x acc = {};
-#pragma unroll
-                for (int s = 0; s < C::NS; s++) {
-                    i4 a = *reinterpret_cast<const i4*>(&sK[(kt * 32 + l32) * C::LD + 32 * s + 16 * g]);
-                    acc = mfma_32x32x32_i8(a, qreg[s], acc);
-                }
-                // s = S * qs * ks * scale * log2e
-#pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    const f4 ks4 = *reinterpret_cast<const f4*>(&ksl[kt * 32 + 8 * r4 + 4 * g]);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        sf[kt][4 * r4 + e] = ((float)acc[4 * r4 + e] * ks4[e]) * qc;
-                    }
-                }
-            }
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        if (do_pv && cls_now != 0) {
+            mfma_stream(T_{}, T_{}, i);
+        } else if (do_pv) {
+            mfma_stream(T_{}, F_{}, i);
+        } else if (cls_now != 0) {
+            mfma_stream(F_{}, T_{}, i);
         }
         cls_prev = cls_now;
     };
 
-    // V(i): exact running max over the 64-key block, P quantised to int8
+    // V(i): dequantise S(i), exact running max over the 64-key block, P as
+    // integers 0..127; O and l are rescaled whenever the max grows
     auto phase_v = [&](int i) {
         if (!wave_active || cls_prev == 0) {
             return;
+        }
+        const float* ksl = sks[i & 1];
+        float t[2][16];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                const f4 ks4 = *reinterpret_cast<const f4*>(&ksl[kt * 32 + 8 * r4 + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    t[kt][4 * r4 + e] = (float)sacc[kt][4 * r4 + e] * ks4[e];
+                }
+            }
+        }
+        if (!qpos) {
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    t[kt][e] *= qc;
+                }
+            }
         }
         if (cls_prev == 2) {
             const int kt0 = (t_begin + i) * kI8BN;
@@ -296,24 +366,24 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
-                    sf[kt][e] = (off < a || off > bnd) ? -INFINITY : sf[kt][e];
+                    t[kt][e] = (off < a || off > bnd) ? -INFINITY : t[kt][e];
                 }
             }
         }
-        float mx = sf[0][0];
+        float mx = t[0][0];
 #pragma unroll
         for (int e = 1; e < 16; e++) {
-            mx = fmaxf(mx, sf[0][e]);
+            mx = fmaxf(mx, t[0][e]);
         }
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            mx = fmaxf(mx, sf[1][e]);
+            mx = fmaxf(mx, t[1][e]);
         }
-        mx = pair_max(mx);
+        mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
         const float m_new = fmaxf(m_run, mx);
         const bool grow = m_new > m_run;
         if (wave_any(grow)) {
-            const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+            const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
             m_run = m_new;
             l_run *= alpha;
 #pragma unroll
@@ -321,18 +391,16 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 oacc[dt] *= alpha;
             }
         }
-        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
         float psum = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
-            uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float pv = fast_exp2(sf[kt][e] - m_use);
-                psum += pv;
-                w[e >> 2] = quant_p(pv, w[e >> 2], e & 3);
+                const float y = fast_exp2(fmaf(t[kt][e], qeff, c0)); // 127 p, at most 127 (+ rounding)
+                psum += y;
+                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
             }
-            pb[kt] = i4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
         }
         l_run += psum;
     };
@@ -377,23 +445,21 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         return;
     }
     const float l = pair_sum(l_run);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float f = l > 0.0f ? p.v_scale / l : 0.0f;
     if (q < p.Sq) {
         _Float16* orow = obase + (int64_t)q * p.o_ss;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; dt++) {
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
-                         (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
+                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * f), (_Float16)(oacc[dt][4 * qq + 1] * f),
+                         (_Float16)(oacc[dt][4 * qq + 2] * f), (_Float16)(oacc[dt][4 * qq + 3] * f)};
                 *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
             }
         }
     }
 }
 
-// Exact int32 S = Q K^T on the same MFMA tiles as the attention kernel's
-// first GEMM; one wave per (32 queries, 32 keys, b*h) tile.
 template <int D>
 __global__ __launch_bounds__(64) void int8_scores_kernel(const int8_t* __restrict__ qp, const int8_t* __restrict__ kp,
                                                         int32_t* __restrict__ out, int64_t q_sb, int64_t q_sh,
@@ -455,7 +521,7 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     p.ksv = a.k_scale_vec;
     p.q_scale = a.q_scale;
     p.k_scale = a.k_scale;
-    p.pv_scale = (1.0f / 127.0f) * a.v_scale;
+    p.v_scale = a.v_scale;
     p.scale_log2e = a.scale * 1.442695041f; // the reference's kLog2E (fa2_forward_int8qk.hip:60)
     p.q_sb = a.qs[0];
     p.q_sh = a.qs[1];
