@@ -395,8 +395,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
     _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
 
+    // Q^T operand (lane holds Q[q][16s + 8g .. +7], RoPE applied); loaded in
+    // the prologue after the first K/V loads are issued so the latencies overlap
     h8 qreg[C::NS];
-    {
+    auto load_q = [&]() {
         const bool valid = q < p.Sq;
         const _Float16* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
 #pragma unroll
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             }
             qreg[s] = x;
         }
-    }
+    };
 
     const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
     int klo, khi;
@@ -626,6 +628,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     // ---- prologue: pair 0 in LDS; each group's registers hold its next pair
     if (n > 0) {
         load_pair(0);
+    }
+    load_q();
+    if (n > 0) {
         store_pair(0);
         load_pair(1);
     }
