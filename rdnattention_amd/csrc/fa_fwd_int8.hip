@@ -188,9 +188,9 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         oacc[dt] = f16x{};
     }
     float m_run = -INFINITY, l_run = 0.0f;
-    i16x sacc[2]; // int32 scores of the current tile
-    sacc[0] = i16x{};
-    sacc[1] = i16x{};
+    f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
+    tsc[0] = f16x{};
+    tsc[1] = f16x{};
     h8 pb[4]; // P^T operands of the four 16-key groups: integers 0..127 in fp16
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -303,8 +303,18 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             __builtin_amdgcn_sched_barrier(0);
         }
         if constexpr (DO_S) {
-            sacc[0] = acc0;
-            sacc[1] = acc1;
+            // dequantise here: the MFMA phase is the shorter one of the two
+            const float* ksl = sks[i & 1];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                const f4 ks0 = *reinterpret_cast<const f4*>(&ksl[8 * r4 + 4 * g]);
+                const f4 ks1 = *reinterpret_cast<const f4*>(&ksl[32 + 8 * r4 + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    tsc[0][4 * r4 + e] = (float)acc0[4 * r4 + e] * ks0[e];
+                    tsc[1][4 * r4 + e] = (float)acc1[4 * r4 + e] * ks1[e];
+                }
+            }
         }
     };
     auto phase_m = [&](int i) {
@@ -329,25 +339,13 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         cls_prev = cls_now;
     };
 
-    // V(i): dequantise S(i), exact running max over the 64-key block, P as
-    // integers 0..127; O and l are rescaled whenever the max grows
+    // V(i): exact running max over the 64-key block, P as integers 0..127;
+    // O and l are rescaled whenever the max grows
     auto phase_v = [&](int i) {
         if (!wave_active || cls_prev == 0) {
             return;
         }
-        const float* ksl = sks[i & 1];
-        float t[2][16];
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const f4 ks4 = *reinterpret_cast<const f4*>(&ksl[kt * 32 + 8 * r4 + 4 * g]);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    t[kt][4 * r4 + e] = (float)sacc[kt][4 * r4 + e] * ks4[e];
-                }
-            }
-        }
+        f16x t[2] = {tsc[0], tsc[1]};
         if (!qpos) {
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
