@@ -164,6 +164,27 @@ __device__ __forceinline__ void row_key_bounds(const MaskSpec& m, int q, int& lo
     visible_key_range(m, q, q, lo, hi);
 }
 
+// Workgroup -> (head group, row tile).  The hardware deals workgroups to the
+// 8 XCDs round-robin (wg % 8), each XCD with its own L2.  With chunk > 0 (and
+// n_hg a multiple of 8 * chunk) each XCD works through `chunk` head groups at
+// a time, all of their row tiles heaviest first, so the K/V those concurrent
+// workgroups stream stays in that XCD's L2; chunk == 0 keeps head groups
+// fastest over the whole grid.
+__device__ __forceinline__ void wg_tile(int wg, int n_hg, int n_rt, int chunk, int& hg, int& rt) {
+    if (chunk > 0) {
+        const int xcd = wg & 7;
+        const int slot = wg >> 3;
+        const int per_chunk = chunk * n_rt;
+        const int c = slot / per_chunk;
+        const int idx = slot - c * per_chunk;
+        rt = n_rt - 1 - idx / chunk;
+        hg = xcd + 8 * (c * chunk + idx % chunk);
+    } else {
+        hg = wg % n_hg;
+        rt = n_rt - 1 - wg / n_hg;
+    }
+}
+
 // Raw buffer resource (gfx9 V#: stride 0, DATA_FORMAT 32): loads at byte
 // offsets >= num_records return 0, which is how rows past the end of K/V read
 // as zeros without per-load branches.

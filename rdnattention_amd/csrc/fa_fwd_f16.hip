@@ -163,8 +163,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     // mask) row tiles are issued first, head groups fastest so that
     // workgroups on one XCD keep sharing the K/V of a kv head
     const int wg = blockIdx.x;
-    const int hg = wg % p.n_head_groups;
-    const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
+    int hg, rt;
+    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
     const int per_b = p.Hkv * p.groups_per_kv;
     const int b = hg / per_b;
     const int rem = hg - b * per_b;
@@ -376,8 +376,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     const int gtid = tid & 255;      // thread index inside the group
 
     const int wg = blockIdx.x;
-    const int hg = wg % p.n_head_groups;
-    const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
+    int hg, rt;
+    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
     const int per_b = p.Hkv * p.groups_per_kv;
     const int b = hg / per_b;
     const int rem = hg - b * per_b;
@@ -713,6 +713,20 @@ int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std
 
 constexpr int64_t kMaxSeqStride = 1 << 24;
 
+int xcd_head_group_chunk(int n_head_groups, int64_t kv_bytes) {
+    constexpr int kXcds = 8;
+    constexpr int64_t kL2Budget = 3 << 20; // of the 4 MB L2 per XCD
+    if (n_head_groups % kXcds != 0 || kv_bytes <= 0) {
+        return 0;
+    }
+    const int per_xcd = n_head_groups / kXcds;
+    int c = (int)std::max<int64_t>(1, std::min<int64_t>(per_xcd, kL2Budget / kv_bytes));
+    while (per_xcd % c != 0) {
+        c--;
+    }
+    return c;
+}
+
 float softmax_log2_scale(float scale) {
     return std::max(std::fabs(scale) * kLog2e, 1e-30f);
 }
@@ -746,6 +760,7 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
     p.n_head_groups = a.B * a.Hkv * p.groups_per_kv;
+    p.hg_chunk = xcd_head_group_chunk(p.n_head_groups, 2 * (int64_t)a.Sk * a.D * (int64_t)sizeof(_Float16));
     p.c = softmax_log2_scale(a.scale);
     p.q_sign = a.scale < 0.0f ? -1.0f : 1.0f;
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};

@@ -185,8 +185,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
     // head groups fastest (as in the other prefill kernels)
     const int wg = blockIdx.x;
     const int dv0 = blockIdx.y == 0 ? 0 : D - C::DV; // this pass's output columns [dv0, dv0 + DV)
-    const int hg = wg % p.n_head_groups;
-    const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
+    int hg, rt;
+    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
     const int per_b = p.Hkv * p.groups_per_kv;
     const int b = hg / per_b;
     const int rem = hg - b * per_b;

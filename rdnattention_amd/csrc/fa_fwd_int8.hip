@@ -30,6 +30,7 @@
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
+#include "fa_prefill.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -63,6 +64,7 @@ struct Int8Params {
     int64_t v_sb, v_sh, v_ss;
     int64_t o_sb, o_sh, o_ss;
     int32_t Hq, Sq, Hkv, ratio, G, rows_per_wg, n_row_tiles, n_head_groups, groups_per_kv;
+    int32_t hg_chunk; // head groups per XCD at a time (0 = head groups fastest)
     MaskSpec mask;
 };
 
@@ -129,8 +131,8 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     const int gtid = tid & 255;
 
     const int wg = blockIdx.x;
-    const int hg = wg % p.n_head_groups;
-    const int rt = p.n_row_tiles - 1 - wg / p.n_head_groups;
+    int hg, rt;
+    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
     const int per_b = p.Hkv * p.groups_per_kv;
     const int b = hg / per_b;
     const int rem = hg - b * per_b;
@@ -542,6 +544,7 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
     p.n_head_groups = a.B * a.Hkv * p.groups_per_kv;
+    p.hg_chunk = xcd_head_group_chunk(p.n_head_groups, 2 * (int64_t)a.Sk * a.D);
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};
     const int64_t n_wg = (int64_t)p.n_row_tiles * p.n_head_groups;
     if (n_wg <= 0 || n_wg > INT32_MAX) {

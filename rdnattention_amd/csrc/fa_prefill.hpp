@@ -27,11 +27,16 @@ struct PrefillParams {
     int32_t n_row_tiles;   // ceil(Sq / rows_per_wg)
     int32_t n_head_groups; // B * Hkv * groups_per_kv
     int32_t groups_per_kv; // ratio / G
+    int32_t hg_chunk;      // head groups per XCD at a time (0 = head groups fastest)
     float c;               // max(|scale| * log2(e), 1e-30)
     float q_sign;          // sign of scale, folded into Q (exact in fp16)
     MaskSpec mask;
     int32_t rope_q;        // rotate Q with rot_cos / rot_sin while loading it
 };
+
+// Head groups an XCD should work through at a time so that their K/V
+// (kv_bytes each) fit its L2; 0 when the grid cannot be dealt evenly.
+int xcd_head_group_chunk(int n_head_groups, int64_t kv_bytes);
 
 // Large-head prefill (head_dim 288..512 in steps of 32), fa_fwd_f16_wide.hip.
 int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
