@@ -71,6 +71,19 @@ __device__ __forceinline__ float pair_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// acc + the sum of the eight halves of v, two per v_dot2c_f32_f16 (fp32
+// accumulation).  Used for the softmax row sum: summing the fp16 P that the
+// P V MFMA consumes keeps numerator and denominator on the same weights.
+__device__ __forceinline__ float sum_h8(h8 v, float acc) {
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const h2 pr = {v[e], v[e + 1]};
+        acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]); the counters not named are left unwaited.
 constexpr int waitcnt_vm(int n) {

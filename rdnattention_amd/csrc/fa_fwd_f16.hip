@@ -128,10 +128,9 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
         h8 pb[2];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const float pv = fast_exp2(fmaf(sacc[kt][i], c, -m_use));
-            psum += pv;
-            pb[i >> 3][i & 7] = (_Float16)pv;
+            pb[i >> 3][i & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][i], c, -m_use));
         }
+        psum = sum_h8(pb[1], sum_h8(pb[0], psum));
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             const int u = 2 * kt + hh; // 16-key group: keys 16u + 4g + {0..3, 8..11}
@@ -617,10 +616,12 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const float pv = fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
-                psum += pv;
-                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)pv;
+                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
             }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            psum = sum_h8(pb[u], psum);
         }
         l_run += psum;
     };

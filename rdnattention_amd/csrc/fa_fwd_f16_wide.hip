@@ -132,10 +132,9 @@ __device__ __forceinline__ void wide_tile(const char* __restrict__ buf, const h8
     float psum = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const float pv = fast_exp2(fmaf(sacc[i], c, -m_use));
-        psum += pv;
-        pb[i >> 3][i & 7] = (_Float16)pv;
+        pb[i >> 3][i & 7] = (_Float16)fast_exp2(fmaf(sacc[i], c, -m_use));
     }
+    psum = sum_h8(pb[1], sum_h8(pb[0], psum));
     l_run += psum;
 
     // O^T += V^T P^T: pb[u] holds keys 16u + 4g + {0..3, 8..11}; the V^T

@@ -275,3 +275,35 @@ def test_large_head_strided_kv_bit_identical(gpu, oracle_lib, d):
     assert torch.equal(o1, o2)
     assert_f16_parity(o1.float().cpu().numpy(), reference_f16(q.cpu(), kv_k.cpu(), kv_v.cpu(), True, -1),
                       f"strided_d{d}")
+
+
+def spike_inputs(seed, b, hq, hkv, s, d, jump, positions):
+    """N(0,1) Q/K/V plus a shared direction u: every query carries 4u and the
+    keys at `positions` carry delta*u, so their scores exceed the typical row
+    max by about `jump` (log2 units) in tiles well after the first."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    q = torch.randn(b, hq, s, d, generator=g) + 4.0 * u
+    k = torch.randn(b, hkv, s, d, generator=g)
+    v = torch.randn(b, hkv, s, d, generator=g)
+    delta = (jump + 4.0) * d ** 0.5 / (4.0 * 1.4426950408889634)
+    for pos in positions:
+        k[:, :, pos] = delta * u
+    return q.half(), k.half(), v.half()
+
+
+@pytest.mark.parametrize("d", [64, 128, 256, 512])
+@pytest.mark.parametrize("jump", [6.0, 12.0, 20.0, 60.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_late_score_spike(gpu, oracle_lib, d, jump, causal):
+    """Row maxima that rise far above the running max in later tiles: the
+    rescale paths (growth inside the lazy margin, beyond it, and beyond the
+    fp16 range of P) must all give the exact softmax."""
+    log(f"[spike] d={d} jump={jump} causal={causal}")
+    q, k, v = spike_inputs(11, 1, 4, 2, 320, d, jump, (150, 251, 300))
+    out = torch.empty_like(q, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal=causal) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, causal, -1)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"spike d{d} jump{jump}")
