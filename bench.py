@@ -234,6 +234,65 @@ def make_step(wl: Workload, dev, host=None):
     raise ValueError(wl.kind)
 
 
+def int8_quantized_e2e(dev, steps: int = 10, warmup: int = 3):
+    """flash_attn_int8qk_quantized on fp16 inputs of the INT8 workload's shape
+    (B=2, Hq=32, Hkv=8, S=8192, D=128, causal), timed whole: this library's
+    path (three quantiser kernels + the INT8 kernel with the per-channel V
+    rescale in its epilogue) against the reference wrapper's composition
+    (rdnattention/__init__.py:303-357: torch quantisers, including the
+    per-tensor Q/K pass it discards, the INT8 kernel, then a torch multiply of
+    the output by v_channel)."""
+    import torch
+
+    import rdnattention_amd as ra
+
+    g = torch.Generator(device=dev).manual_seed(7)
+    b, hq, hkv, s, d = 2, 32, 8, 8192, 128
+    q = torch.randn(b, hq, s, d, device=dev, generator=g).half()
+    k = torch.randn(b, hkv, s, d, device=dev, generator=g).half()
+    v = torch.randn(b, hkv, s, d, device=dev, generator=g).half()
+
+    def torch_composition():
+        def per_tensor(x):
+            sc = x.abs().max().item() / 127.0
+            sc = sc if sc != 0.0 else 1.0
+            return torch.clamp(torch.round(x / sc), -127, 127).to(torch.int8), sc
+
+        def per_token(x):
+            x = x.float()
+            sc = x.abs().amax(dim=-1, keepdim=True) / 127.0
+            sc = torch.where(sc == 0, torch.ones_like(sc), sc)
+            return torch.clamp(torch.round(x / sc), -127, 127).to(torch.int8), sc.squeeze(-1).contiguous()
+
+        per_tensor(q.float())
+        per_tensor(k.float())
+        vf = v.float()
+        vc = vf.abs().amax(dim=-2, keepdim=True) / 127.0
+        vc = torch.where(vc == 0, torch.ones_like(vc), vc)
+        vi = torch.clamp(torch.round(vf / vc), -127, 127).to(torch.int8)
+        qi, qs = per_token(q)
+        ki, ks = per_token(k)
+        out = ra.flash_attn_int8qk(qi, ki, vi, qs, ks, 1.0, True)
+        return (out.float() * vc.repeat_interleave(hq // hkv, dim=1)).to(out.dtype)
+
+    def fused():
+        return ra.flash_attn_int8qk_quantized(q, k, v, is_causal=True)
+
+    res = {}
+    for name, fn in (("fused_ms", fused), ("torch_composition_ms", torch_composition)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        res[name] = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+    res["speedup"] = round(res["torch_composition_ms"] / res["fused_ms"], 2)
+    res["shape"] = "fp16 Q [2,32,8192,128], K/V [2,8,8192,128], causal"
+    return res
+
+
 def time_steps(step, steps: int, warmup: int):
     """Runs `warmup` untimed steps, then `steps` timed ones bracketed by
     device synchronisation; returns (ms per step, mean kernel ms, launches, wall s)."""
@@ -471,6 +530,11 @@ def main(argv=None):
         f16 = secondary.get("fp16_causal_gqa_b2_h32_kv8_s8192_d128", {})
         if "kernel_ms" in i8 and "kernel_ms" in f16:
             secondary["int8_over_fp16_same_shape"] = round(f16["kernel_ms"] / i8["kernel_ms"], 3)
+        try:
+            secondary["int8_quantized_end_to_end"] = int8_quantized_e2e(dev)
+        except ra.RDNAttentionError as e:
+            secondary["int8_quantized_end_to_end"] = {"error": str(e)}
+        torch.cuda.empty_cache()
 
     cpu = sdpa = None
     if not args.no_cpu and host is not None:

@@ -42,6 +42,44 @@ RDNA_API int32_t rdna_int8_qk_scores(
     uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
     void* hip_stream);
 
+/* rdna_attention_forward_int8qk() with a per-channel V scale applied inside
+ * the kernel: output = softmax-weighted sum of v_i8 * v_scale *
+ * v_channel_vec[b, kv_head, d], where v_channel_vec is a contiguous fp32
+ * [batch, num_kv_heads, head_dim] device array (16-byte aligned), or null for
+ * the plain per-tensor v_scale.  No reference counterpart: the reference's
+ * flash_attn_int8qk_quantized (rdnattention/__init__.py:346-357) multiplies
+ * the kernel's fp16 output by v_channel in a separate torch pass; here that
+ * product is part of the kernel's epilogue. */
+RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
+    const void* q, const void* k, const void* v, void* output,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads,
+    uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
+    float scale, float q_scale, float k_scale, float v_scale,
+    const void* q_scale_vec, const void* k_scale_vec, const void* v_channel_vec,
+    int32_t causal, int32_t window_size, void* hip_stream);
+
+/* INT8 quantisation on the GPU, bit-identical to the reference wrapper's
+ * torch ops (rdnattention/__init__.py:303-343):
+ *   per_channel == 0 (per token): scale[b,h,s] = max_d |x| / 127 (0 -> 1)
+ *   per_channel != 0 (per channel): scale[b,h,d] = max_s |x| / 127 (0 -> 1)
+ *   q = clamp(round_half_even(x / scale), -127, 127)
+ * x: fp16 (x_dtype 0) or fp32 (x_dtype 1) [batch, num_heads, seq_len,
+ * head_dim] with element strides (b, h, s) and unit stride along head_dim;
+ * 16-byte aligned, strides multiples of 16 bytes; head_dim a multiple of 8
+ * up to 512.  q_out: int8 [batch, num_heads, seq_len, head_dim] contiguous;
+ * scale_out: fp32, [batch, num_heads, seq_len] or [batch, num_heads,
+ * head_dim], contiguous.  Returns 0, or -3 with "Quantize (int8) failed: ...".
+ * No reference counterpart (the reference quantises with torch ops). */
+RDNA_API int32_t rdna_quantize_int8(
+    const void* x, int32_t x_dtype,
+    int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t seq_len, uint32_t head_dim,
+    int32_t per_channel, void* q_out, void* scale_out, void* hip_stream);
+
 /* Kernel timer.  While enabled, each launch of a main attention kernel
  * (prefill, split-K, int8; not the RoPE pre-rotation or split-K combine
  * kernels) is bracketed by a HIP event pair recorded on its stream.

@@ -86,6 +86,10 @@ def _lib_handle():
         lib.rdna_attention_forward_path.restype = _I32
         lib.rdna_attention_forward_int8qk.argtypes = _I8_ARGS
         lib.rdna_attention_forward_int8qk.restype = _I32
+        lib.rdna_attention_forward_int8qk_vchannel.argtypes = _I8_ARGS[:-3] + [_VP] + _I8_ARGS[-3:]
+        lib.rdna_attention_forward_int8qk_vchannel.restype = _I32
+        lib.rdna_quantize_int8.argtypes = [_VP, _I32] + [_I64] * 3 + [_U32] * 4 + [_I32, _VP, _VP, _VP]
+        lib.rdna_quantize_int8.restype = _I32
         lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
         lib.rdna_int8_qk_scores.restype = _I32
         lib.rdna_kernel_timer_enable.argtypes = [_I32]
@@ -295,7 +299,8 @@ def flash_attn_int8qk(query, key, value, q_scale, k_scale, v_scale: float, is_ca
 
 
 def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_scale: float, *,
-                                is_causal: bool = False, window_size: int = -1, scale=None) -> None:
+                                is_causal: bool = False, window_size: int = -1, scale=None,
+                                v_channel=None) -> None:
     """INT8 forward written into a preallocated float16 `output` (the raw
     rdna_attention_forward_int8qk call, src/c_api.cpp:116-195).
 
@@ -303,7 +308,10 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
     contiguous head_dim axis and batch/head/seq strides that are multiples of
     16 elements.  q_scale/k_scale: floats, or contiguous float32 device
     tensors of per-token scales [batch, heads, seq_len] /
-    [batch, kv_heads, key_seq_len].  Asynchronous on torch's current stream."""
+    [batch, kv_heads, key_seq_len].  v_channel: optional contiguous float32
+    device tensor [batch, kv_heads, head_dim] of per-channel V scales applied
+    in the kernel (rdna_attention_forward_int8qk_vchannel).  Asynchronous on
+    torch's current stream."""
     import torch
 
     for name, t in (("query", query), ("key", key), ("value", value)):
@@ -324,13 +332,20 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
     q_scalar, q_vec = _scale_arg(q_scale, "q_scale", (batch, heads, seq_len))
     k_scalar, k_vec = _scale_arg(k_scale, "k_scale", (batch, kv_heads, key_seq_len))
     qs, ks, vs, os_ = query.stride(), key.stride(), value.stride(), output.stride()
-    result = _lib_handle().rdna_attention_forward_int8qk(
-        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
-        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
-        batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
-        float(head_dim ** -0.5 if scale is None else scale), q_scalar, k_scalar, float(v_scale),
-        q_vec.data_ptr() if q_vec is not None else None, k_vec.data_ptr() if k_vec is not None else None,
-        1 if is_causal else 0, int(window_size), _stream())
+    args = [query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+            qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os_[0], os_[1], os_[2],
+            batch, heads, kv_heads, seq_len, key_seq_len, head_dim,
+            float(head_dim ** -0.5 if scale is None else scale), q_scalar, k_scalar, float(v_scale),
+            q_vec.data_ptr() if q_vec is not None else None, k_vec.data_ptr() if k_vec is not None else None]
+    tail = [1 if is_causal else 0, int(window_size), _stream()]
+    if v_channel is None:
+        result = _lib_handle().rdna_attention_forward_int8qk(*args, *tail)
+    else:
+        want = (batch, kv_heads, head_dim)
+        if (not isinstance(v_channel, torch.Tensor) or v_channel.dtype != torch.float32
+                or not v_channel.is_contiguous() or tuple(v_channel.shape) != want or not v_channel.is_cuda):
+            raise ValueError(f"v_channel must be a contiguous float32 HIP tensor of shape {want}")
+        result = _lib_handle().rdna_attention_forward_int8qk_vchannel(*args, v_channel.data_ptr(), *tail)
     if result != 0:
         raise RDNAttentionError(f"attention_int8_forward_into failed: {last_error()}")
 
@@ -366,11 +381,44 @@ class KernelTimer:
         return False
 
 
+def _quantize_gpu(x, per_channel: bool):
+    """rdna_quantize_int8 on a HIP tensor [B, H, S, D]: (int8 [B, H, S, D]
+    contiguous, float32 scales [B, H, S] per token or [B, H, D] per channel),
+    bit-identical to the torch formulas of the reference wrapper."""
+    import torch
+
+    if x.dim() != 4:
+        raise ValueError(f"expected a 4D [batch, heads, seq, head_dim] tensor, got shape {tuple(x.shape)}")
+    if x.dtype not in (torch.float16, torch.float32):
+        x = x.float()
+    dt = 0 if x.dtype == torch.float16 else 1
+    mult = 8 if dt == 0 else 4
+    if x.stride(-1) != 1 or any(st % mult for st in x.stride()[:3]) or x.data_ptr() % 16:
+        x = x.contiguous()
+    b, h, s, d = x.shape
+    if d % 8 != 0 or d > 512:
+        raise RDNAttentionError(f"GPU quantiser: head_dim {d} must be a multiple of 8 up to 512")
+    q = torch.empty((b, h, s, d), dtype=torch.int8, device=x.device)
+    sc = torch.ones((b, h, d) if per_channel else (b, h, s), dtype=torch.float32, device=x.device)
+    if q.numel() == 0:
+        return q, sc
+    st = x.stride()
+    rc = _lib_handle().rdna_quantize_int8(x.data_ptr(), dt, st[0], st[1], st[2], b, h, s, d, 1 if per_channel else 0,
+                                          q.data_ptr(), sc.data_ptr(), _stream())
+    if rc != 0:
+        raise RDNAttentionError(f"quantisation failed: {last_error()}")
+    return q, sc
+
+
 def quantize_int8_perchannel_v(query, key, value):
     """(qi, ki, vi, q_scale, k_scale, v_scale, v_channel) with per-tensor Q/K
     scales and one V scale per (batch, kv head, channel); v_scale = 1.0
     (rdnattention/__init__.py:303-324).  Attention is linear in V, so
-    multiplying the output by v_channel undoes the V scaling exactly."""
+    multiplying the output by v_channel undoes the V scaling exactly.
+
+    On HIP tensors the per-channel V pass runs as a library kernel
+    (rdna_quantize_int8); the per-tensor Q/K scales stay torch reductions.
+    CPU tensors go through the same formulas in torch."""
     import torch
 
     def per_tensor(x):
@@ -380,6 +428,9 @@ def quantize_int8_perchannel_v(query, key, value):
 
     qi, q_scale = per_tensor(query.float())
     ki, k_scale = per_tensor(key.float())
+    if value.is_cuda:
+        vi, v_channel = _quantize_gpu(value, per_channel=True)
+        return qi, ki, vi, q_scale, k_scale, 1.0, v_channel
     v = value.float()
     v_channel = v.abs().amax(dim=-2, keepdim=True) / 127.0
     v_channel = torch.where(v_channel == 0, torch.ones_like(v_channel), v_channel)
@@ -389,8 +440,15 @@ def quantize_int8_perchannel_v(query, key, value):
 
 def quantize_int8_qk_pertoken(query, key):
     """(qi, ki, q_scale, k_scale) with one fp32 scale per (batch, head, row)
-    (rdnattention/__init__.py:327-343)."""
+    (rdnattention/__init__.py:327-343).  HIP tensors are quantised by a
+    library kernel (rdna_quantize_int8), bit-identical to the torch formulas
+    used for CPU tensors."""
     import torch
+
+    if query.is_cuda and key.is_cuda:
+        qi, q_scale = _quantize_gpu(query, per_channel=False)
+        ki, k_scale = _quantize_gpu(key, per_channel=False)
+        return qi, ki, q_scale, k_scale
 
     def per_token(x):
         x = x.float()
@@ -405,19 +463,45 @@ def quantize_int8_qk_pertoken(query, key):
 
 def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, window_size: int = -1):
     """INT8 attention from ordinary fp16/fp32 Q/K/V (rdnattention/__init__.py:346-357):
-    per-token Q/K scales in-kernel and an exact per-channel V rescale after it.
+    per-token Q/K scales and a per-channel V scale.
 
-    Differs from the reference in one respect: v_channel is indexed by the kv
-    head of each query head, so grouped-query inputs with 1 < kv_heads < heads
-    work (the reference's broadcast raises there)."""
-    _, _, vi, _, _, v_scale, v_channel = quantize_int8_perchannel_v(query, key, value)
-    qi, ki, q_scale, k_scale = quantize_int8_qk_pertoken(query, key)
-    out = flash_attn_int8qk(qi.contiguous(), ki.contiguous(), vi.contiguous(), q_scale, k_scale, v_scale,
-                            is_causal, window_size)
-    ratio = query.shape[1] // key.shape[1]
-    if ratio > 1:
-        v_channel = v_channel.repeat_interleave(ratio, dim=1)
-    return (out.float() * v_channel.unsqueeze(-2)).to(out.dtype)
+    Three quantiser kernels and one attention kernel: the per-channel V
+    rescale is applied in the attention kernel's epilogue
+    (rdna_attention_forward_int8qk_vchannel) instead of a separate pass over
+    the output, and the per-tensor Q/K quantisation the reference computes and
+    discards is skipped.  The output is rounded to fp16 once (the reference
+    rounds the kernel output, then the rescaled product).
+
+    Differs from the reference in one more respect: v_channel is indexed by
+    the kv head of each query head, so grouped-query inputs with
+    1 < kv_heads < heads work (the reference's broadcast raises there)."""
+    import torch
+
+    for name, t in (("query", query), ("key", key), ("value", value)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError("requires torch.Tensor inputs (GPU tensors already on this device)")
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be on a HIP device")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4D [batch, heads, seq, head_dim], got shape {tuple(t.shape)}")
+    if query.shape[0] != key.shape[0] or query.shape[0] != value.shape[0]:
+        raise ValueError(f"Batch size must match: Q={query.shape}, K={key.shape}, V={value.shape}")
+    heads, kv_heads = query.shape[1], key.shape[1]
+    if kv_heads == 0 or heads % kv_heads != 0:
+        raise RDNAttentionError(
+            f"flash_attn_int8qk: query heads ({heads}) must be a positive multiple of key/value heads ({kv_heads})")
+    _check_head_dim(query.shape[-1], "flash_attn_int8qk", allowed=SUPPORTED_HEAD_DIMS_INT8)
+    if not has_device():
+        raise RDNAttentionError("no usable HIP device found")
+    qi, q_scale = _quantize_gpu(query, per_channel=False)
+    ki, k_scale = _quantize_gpu(key, per_channel=False)
+    vi, v_channel = _quantize_gpu(value, per_channel=True)
+    output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
+    if output.numel() == 0:
+        return output
+    attention_int8_forward_into(qi, ki, vi, output, q_scale, k_scale, 1.0, is_causal=is_causal,
+                                window_size=window_size, v_channel=v_channel)
+    return output
 
 
 __all__ = ["flash_attn", "flash_attn_int8qk", "flash_attn_int8qk_quantized", "quantize_int8_perchannel_v",

@@ -126,8 +126,8 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
                         int64_t qss, int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss,
                         int64_t osb, int64_t osh, int64_t oss, uint32_t B, uint32_t Hq, uint32_t Hkv, uint32_t Sq,
                         uint32_t Sk, uint32_t D, float scale, float q_scale, float k_scale, float v_scale,
-                        const void* q_scale_vec, const void* k_scale_vec, int32_t causal, int32_t window,
-                        void* stream, std::string& err) {
+                        const void* q_scale_vec, const void* k_scale_vec, const void* v_channel_vec,
+                        int32_t causal, int32_t window, void* stream, std::string& err) {
     // order of the reference's checks: ratio, then head_dim (fa2_forward_int8qk.hip:570-589)
     if (Hkv == 0 || Hq % Hkv != 0) {
         err = "numHeads must be a positive multiple of numKvHeads";
@@ -154,6 +154,10 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
         err = "q_scale_vec/k_scale_vec must be 4-byte aligned float arrays";
         return -1;
     }
+    if (!aligned(v_channel_vec, 16)) {
+        err = "v_channel_vec must be a 16-byte aligned float array";
+        return -1;
+    }
     a.B = (int32_t)B;
     a.Hq = (int32_t)Hq;
     a.Hkv = (int32_t)Hkv;
@@ -168,6 +172,7 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
     a.v_scale = v_scale;
     a.q_scale_vec = static_cast<const float*>(q_scale_vec);
     a.k_scale_vec = static_cast<const float*>(k_scale_vec);
+    a.v_channel = static_cast<const float*>(v_channel_vec);
     return rdna_amd::fwd_int8(a, static_cast<hipStream_t>(stream), err);
 }
 
@@ -252,13 +257,83 @@ RDNA_API int32_t rdna_attention_forward_int8qk(const void* q, const void* k, con
     int rc = forward_i8_impl(q, k, v, output, q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s,
                              v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h, o_stride_s, batch_size,
                              num_heads, num_kv_heads, seq_len, key_seq_len, head_dim, scale, q_scale, k_scale,
-                             v_scale, q_scale_vec, k_scale_vec, causal, window_size, hip_stream, err);
+                             v_scale, q_scale_vec, k_scale_vec, nullptr, causal, window_size, hip_stream, err);
     if (rc != 0) {
         set_error("Attention (int8qk) failed: %s", err);
         return -3;
     }
     return 0;
 #endif
+}
+
+RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
+    const void* q, const void* k, const void* v, void* output, int64_t q_stride_b, int64_t q_stride_h,
+    int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s, int64_t v_stride_b,
+    int64_t v_stride_h, int64_t v_stride_s, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads, uint32_t seq_len, uint32_t key_seq_len,
+    uint32_t head_dim, float scale, float q_scale, float k_scale, float v_scale, const void* q_scale_vec,
+    const void* k_scale_vec, const void* v_channel_vec, int32_t causal, int32_t window_size, void* hip_stream) {
+#if defined(RDNATTENTION_NO_INT8)
+    (void)q, (void)k, (void)v, (void)output, (void)q_stride_b, (void)q_stride_h, (void)q_stride_s;
+    (void)k_stride_b, (void)k_stride_h, (void)k_stride_s, (void)v_stride_b, (void)v_stride_h, (void)v_stride_s;
+    (void)o_stride_b, (void)o_stride_h, (void)o_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads;
+    (void)seq_len, (void)key_seq_len, (void)head_dim, (void)scale, (void)q_scale, (void)k_scale, (void)v_scale;
+    (void)q_scale_vec, (void)k_scale_vec, (void)v_channel_vec, (void)causal, (void)window_size, (void)hip_stream;
+    set_error("Attention (int8qk) unavailable: %s",
+              "this library was built without the INT8 kernel - use rdna_attention_forward() instead");
+    return -4;
+#else
+    std::string err;
+    int rc = forward_i8_impl(q, k, v, output, q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s,
+                             v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h, o_stride_s, batch_size,
+                             num_heads, num_kv_heads, seq_len, key_seq_len, head_dim, scale, q_scale, k_scale,
+                             v_scale, q_scale_vec, k_scale_vec, v_channel_vec, causal, window_size, hip_stream, err);
+    if (rc != 0) {
+        set_error("Attention (int8qk) failed: %s", err);
+        return -3;
+    }
+    return 0;
+#endif
+}
+
+RDNA_API int32_t rdna_quantize_int8(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_h,
+                                    int64_t x_stride_s, uint32_t batch_size, uint32_t num_heads, uint32_t seq_len,
+                                    uint32_t head_dim, int32_t per_channel, void* q_out, void* scale_out,
+                                    void* hip_stream) {
+    std::string err;
+    const int64_t mult = x_dtype == 1 ? 4 : 8; // elements per 16 bytes
+    if (x_dtype != 0 && x_dtype != 1) {
+        err = "x_dtype must be 0 (fp16) or 1 (fp32)";
+    } else if (head_dim < 8 || head_dim > 512 || head_dim % 8 != 0) {
+        err = "head_dim must be a multiple of 8 from 8 to 512";
+    } else if (batch_size == 0 || num_heads == 0 || seq_len == 0) {
+        err = "empty tensor (batch_size, num_heads and seq_len must be non-zero)";
+    } else if (seq_len > kMaxSeq || (uint64_t)batch_size * num_heads > (uint64_t)INT32_MAX / 2) {
+        err = "tensor dimensions exceed the supported range";
+    } else if (x == nullptr || q_out == nullptr || scale_out == nullptr) {
+        err = "null tensor pointer";
+    } else if (!aligned(x, 16) || !aligned(q_out, 16) || !aligned(scale_out, 4)) {
+        err = "x and q_out must be 16-byte aligned, scale_out 4-byte aligned";
+    } else if (x_stride_b % mult != 0 || x_stride_h % mult != 0 || x_stride_s % mult != 0) {
+        err = "batch/head/seq strides of x must be multiples of 16 bytes";
+    } else {
+        rdna_amd::QuantArgs a;
+        a.x = x;
+        a.x_fp32 = x_dtype == 1 ? 1 : 0;
+        a.xs[0] = x_stride_b, a.xs[1] = x_stride_h, a.xs[2] = x_stride_s;
+        a.B = (int32_t)batch_size;
+        a.H = (int32_t)num_heads;
+        a.S = (int32_t)seq_len;
+        a.D = (int32_t)head_dim;
+        a.per_channel = per_channel != 0 ? 1 : 0;
+        a.q = q_out;
+        a.scale = static_cast<float*>(scale_out);
+        if (rdna_amd::quantize_int8(a, static_cast<hipStream_t>(hip_stream), err) == 0) {
+            return 0;
+        }
+    }
+    set_error("Quantize (int8) failed: %s", err);
+    return -3;
 }
 
 RDNA_API int32_t rdna_int8_qk_scores(const void* q, const void* k, int32_t* scores, int64_t q_stride_b,
@@ -333,7 +408,7 @@ int forwardInt8QK(const ForwardParamsInt8QK& p, void* stream) {
     int rc = forward_i8_impl(p.q, p.k, p.v, p.o, p.qStrideB, p.qStrideH, p.qStrideS, p.kStrideB, p.kStrideH,
                              p.kStrideS, p.vStrideB, p.vStrideH, p.vStrideS, p.oStrideB, p.oStrideH, p.oStrideS,
                              p.batchSize, p.numHeads, p.numKvHeads, p.seqLen, p.keySeqLen, p.headDim, p.scale,
-                             p.qScale, p.kScale, p.vScale, p.qScaleVec, p.kScaleVec, (int32_t)p.causal,
+                             p.qScale, p.kScale, p.vScale, p.qScaleVec, p.kScaleVec, nullptr, (int32_t)p.causal,
                              p.windowSize, stream, err);
     if (rc != 0) {
         std::snprintf(g_last_i8, sizeof(g_last_i8), "%s", err.c_str());

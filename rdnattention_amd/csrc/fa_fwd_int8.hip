@@ -56,6 +56,7 @@ struct Int8Params {
     _Float16* o;
     const float* qsv; // [B, Hq, Sq] or null
     const float* ksv; // [B, Hkv, Sk] or null
+    const float* vch; // [B, Hkv, D] per-channel V scale or null
     float q_scale, k_scale;
     float v_scale;
     float scale_log2e;
@@ -448,13 +449,25 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     const float f = l > 0.0f ? p.v_scale / l : 0.0f;
     if (q < p.Sq) {
         _Float16* orow = obase + (int64_t)q * p.o_ss;
+        // per-channel V scale of this kv head (1 when absent)
+        const float* vch = p.vch != nullptr ? p.vch + ((int64_t)b * p.Hkv + kvh) * D : nullptr;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; dt++) {
 #pragma unroll
             for (int qq = 0; qq < 4; qq++) {
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * f), (_Float16)(oacc[dt][4 * qq + 1] * f),
-                         (_Float16)(oacc[dt][4 * qq + 2] * f), (_Float16)(oacc[dt][4 * qq + 3] * f)};
-                *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
+                const int d0 = dt * 32 + 8 * qq + 4 * g;
+                float c[4] = {f, f, f, f};
+                if (vch != nullptr) {
+                    typedef float f4 __attribute__((ext_vector_type(4)));
+                    const f4 w = *reinterpret_cast<const f4*>(vch + d0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        c[e] = f * w[e];
+                    }
+                }
+                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * c[0]), (_Float16)(oacc[dt][4 * qq + 1] * c[1]),
+                         (_Float16)(oacc[dt][4 * qq + 2] * c[2]), (_Float16)(oacc[dt][4 * qq + 3] * c[3])};
+                *reinterpret_cast<h4*>(orow + d0) = o4;
             }
         }
     }
@@ -519,6 +532,7 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     p.o = static_cast<_Float16*>(a.o);
     p.qsv = a.q_scale_vec;
     p.ksv = a.k_scale_vec;
+    p.vch = a.v_channel;
     p.q_scale = a.q_scale;
     p.k_scale = a.k_scale;
     p.v_scale = a.v_scale;

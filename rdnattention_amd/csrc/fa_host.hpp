@@ -31,6 +31,22 @@ struct AttnArgs {
     float q_scale = 1.0f, k_scale = 1.0f, v_scale = 1.0f;
     const float* q_scale_vec = nullptr;
     const float* k_scale_vec = nullptr;
+    // per-channel V scale [B, Hkv, D] (contiguous) multiplied into the output,
+    // or null
+    const float* v_channel = nullptr;
+};
+
+// INT8 quantiser arguments: x fp16 or fp32 [B, H, S, D] (element strides
+// b, h, s; unit stride along D) -> q int8 [B, H, S, D] contiguous and fp32
+// scales, [B, H, S] per token or [B, H, D] per channel.
+struct QuantArgs {
+    const void* x = nullptr;
+    int32_t x_fp32 = 0;
+    int64_t xs[3] = {0, 0, 0};
+    int32_t B = 0, H = 0, S = 0, D = 0;
+    int32_t per_channel = 0;
+    void* q = nullptr;
+    float* scale = nullptr;
 };
 
 // Kernel paths the FP16 dispatcher can take.
@@ -41,6 +57,9 @@ int fwd_f16(const AttnArgs& a, F16Path path, hipStream_t stream, std::string& er
 
 // INT8 forward (both GEMMs on int8 MFMA).  Returns 0 or sets `err`.
 int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err);
+
+// INT8 quantisation on the GPU (fa_quant.hip).  Returns 0 or sets `err`.
+int quantize_int8(const QuantArgs& a, hipStream_t stream, std::string& err);
 
 // Test export: exact int32 S = Q_i8 K_i8^T into `scores` [B,Hq,Sq,Sk] (contiguous).
 int int8_scores(const AttnArgs& a, int32_t* scores, hipStream_t stream, std::string& err);

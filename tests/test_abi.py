@@ -199,3 +199,38 @@ def test_kernel_timer_without_launches(lib):
     assert ms.value == 0.0 and n.value == 0
     assert lib.rdna_kernel_timer_read(None, None) == -3
     assert lib.rdna_kernel_timer_enable(0) == 0
+
+
+def _quant(lib, **kw):
+    hold, p = _buf()
+    args = dict(x=p, dtype=0, strides=(8 * 16 * 64, 16 * 64, 64), B=1, H=8, S=16, D=64, per_channel=0, q=p, sc=p)
+    args.update(kw)
+    s = args["strides"]
+    rc = lib.rdna_quantize_int8(args["x"], args["dtype"], *s, args["B"], args["H"], args["S"], args["D"],
+                                args["per_channel"], args["q"], args["sc"], None)
+    return rc, lib.rdna_get_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=12), "head_dim must be a multiple of 8 from 8 to 512"),
+    (dict(D=520), "head_dim must be a multiple of 8 from 8 to 512"),
+    (dict(dtype=2), "x_dtype must be 0 (fp16) or 1 (fp32)"),
+    (dict(S=0), "empty tensor"),
+    (dict(x=None), "null tensor pointer"),
+    (dict(strides=(8192, 1024, 68)), "strides of x must be multiples of 16 bytes"),
+    (dict(dtype=1, strides=(8192, 1024, 66)), "strides of x must be multiples of 16 bytes"),
+])
+def test_quantize_argument_errors(lib, kw, msg):
+    rc, err = _quant(lib, **kw)
+    assert rc == -3
+    assert err.startswith("Quantize (int8) failed: ")
+    assert msg in err
+
+
+def test_int8_vchannel_misaligned_rejected(lib):
+    hold, p = _buf()
+    s = (8 * 8 * 64, 8 * 64, 64)
+    rc = lib.rdna_attention_forward_int8qk_vchannel(p, p, p, p, *s, *s, *s, *s, 1, 8, 8, 8, 8, 64, 0.125, 1.0, 1.0,
+                                                     1.0, None, None, p + 4, 0, -1, None)
+    assert rc == -3
+    assert "v_channel_vec must be a 16-byte aligned float array" in lib.rdna_get_error().decode()
