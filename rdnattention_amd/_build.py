@@ -4,7 +4,8 @@
 
 Objects go to rdnattention_amd/_build/, the library to
 rdnattention_amd/lib/librdnattention.so (in-tree, so it travels with the
-repository snapshot to the GPU machine).  Mirrors the reference's build
+repository snapshot to the GPU machine), and the compiler's per-kernel
+resource usage to rdnattention_amd/lib/kernel_resources.json.  Mirrors the reference's build
 options (CMakeLists.txt:3-5 forced Release, :33 RDNATTENTION_ENABLE_INT8)
 for one architecture, gfx950.
 """
@@ -12,7 +13,9 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -24,6 +27,9 @@ CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB_DIR = PKG / "lib"
 LIB = LIB_DIR / "librdnattention.so"
+# per-kernel resource usage of the last build (VGPRs, AGPRs, scratch, LDS,
+# occupancy), from the compiler's kernel-resource-usage remarks
+RESOURCES = LIB_DIR / "kernel_resources.json"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in device code (the host pass
@@ -36,11 +42,29 @@ def sources():
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(src: Path, arch: str, defines, verbose: bool) -> Path:
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]"
+                     r"|LDS Size \[bytes/block\]|TotalSGPRs): (\S+)")
+_KEYS = {"VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch_bytes_per_lane",
+         "Occupancy [waves/SIMD]": "waves_per_simd", "LDS Size [bytes/block]": "lds_bytes", "TotalSGPRs": "sgprs"}
+
+
+def parse_resource_remarks(text: str, source: str):
+    """Kernel-resource-usage remarks -> [{"kernel", "source", "vgprs", ...}]."""
+    kernels = []
+    for m in _REMARK.finditer(text):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            kernels.append({"kernel": val, "source": source})
+        elif kernels:
+            kernels[-1][_KEYS[key]] = int(val)
+    return kernels
+
+
+def _compile(src: Path, arch: str, defines, verbose: bool):
     out = OBJ / (src.name + ".o")
     if src.suffix == ".hip":
-        cmd = [HIPCC, "-x", "hip", f"--offload-arch={arch}", *COMMON, *DEVICE_FLAGS, *defines, "-c", str(src),
-               "-o", str(out)]
+        cmd = [HIPCC, "-x", "hip", f"--offload-arch={arch}", *COMMON, *DEVICE_FLAGS, *defines,
+               "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(out)]
     else:
         cmd = [HIPCC, "-x", "c++", *COMMON, "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", *defines, "-c",
                str(src), "-o", str(out)]
@@ -50,10 +74,10 @@ def _compile(src: Path, arch: str, defines, verbose: bool) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
     if verbose and r.stderr.strip():
-        lines = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        lines = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln and "remark:" not in ln]
         if lines:
             print("\n".join(lines), file=sys.stderr)
-    return out
+    return out, parse_resource_remarks(r.stderr, src.name)
 
 
 def build(arch: str = "gfx950", int8: bool = True, verbose: bool = False, jobs: int | None = None) -> Path:
@@ -63,7 +87,9 @@ def build(arch: str = "gfx950", int8: bool = True, verbose: bool = False, jobs: 
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, arch, defines, verbose), srcs))
+        results = list(ex.map(lambda s: _compile(s, arch, defines, verbose), srcs))
+    objs = [o for o, _ in results]
+    RESOURCES.write_text(json.dumps([k for _, ks in results for k in ks], indent=1))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={arch}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:

@@ -1,0 +1,85 @@
+"""Resource audit of every gfx950 kernel in the last build (CPU only).
+
+rdnattention_amd/_build.py records the compiler's kernel-resource-usage
+remarks in rdnattention_amd/lib/kernel_resources.json.  This test holds the
+kernels to what their launches assume (the reference audits its own tile
+choices against a VGPR cap, tests/head_dim_resources.py):
+
+* no register spills (scratch 0 bytes per lane);
+* LDS per workgroup within gfx950's 160 KiB;
+* enough occupancy for the waves one workgroup places on a SIMD (the
+  8-wave kernels need 2 waves per SIMD, the 4-wave ones 1);
+* every head dim the dispatchers can select is compiled in.
+"""
+import json
+import re
+
+import pytest
+
+from rdnattention_amd import _build
+
+LDS_LIMIT = 160 * 1024
+
+# kernel name fragment -> waves of one workgroup per SIMD (workgroup waves / 4)
+WAVES_PER_SIMD = {
+    "fa_fwd_f16_pp": 2,
+    "fa_fwd_int8": 2,
+    "fa_fwd_f16_prefill": 1,
+    "fa_fwd_f16_wide": 1,
+    "fa_fwd_f16_decode": 1,
+}
+
+
+@pytest.fixture(scope="module")
+def kernels():
+    if not _build.RESOURCES.exists() or not _build.LIB.exists():
+        _build.build()
+    ks = json.loads(_build.RESOURCES.read_text())
+    assert ks, "no kernel resources recorded"
+    return ks
+
+
+def _demangled_base(name):
+    m = re.search(r"N_1\d+(\w+?)I", name) or re.search(r"N_1\d+(\w+?)E", name)
+    return m.group(1) if m else name
+
+
+def test_no_spills(kernels):
+    spills = [(k["kernel"], k["scratch_bytes_per_lane"]) for k in kernels if k.get("scratch_bytes_per_lane", 0)]
+    assert not spills, spills
+
+
+def test_lds_within_gfx950_limit(kernels):
+    over = [(k["kernel"], k["lds_bytes"]) for k in kernels if k["lds_bytes"] > LDS_LIMIT]
+    assert not over, over
+
+
+def test_occupancy_fits_the_workgroup(kernels):
+    checked = 0
+    for k in kernels:
+        need = WAVES_PER_SIMD.get(_demangled_base(k["kernel"]))
+        if need is not None:
+            assert k["waves_per_simd"] >= need, (k["kernel"], k["waves_per_simd"], need)
+            checked += 1
+    assert checked >= 4 + 4 + 8 + 3 + 2
+
+
+def test_every_dispatched_head_dim_is_compiled(kernels):
+    names = [k["kernel"] for k in kernels]
+
+    def has(base, d):
+        return any(f"{base}ILi{d}E" in n for n in names)
+
+    for d in (32, 64, 96, 128):
+        assert has("fa_fwd_f16_pp", d), d
+    for d in (160, 192, 224, 256):
+        assert has("fa_fwd_f16_prefill", d), d
+    for d in range(288, 513, 32):
+        assert has("fa_fwd_f16_wide", d), d
+    for d in (32, 64, 128):
+        assert has("fa_fwd_f16_decode", d), d
+    for d in (64, 128):
+        assert has("fa_fwd_int8", d), d
+    for frag in ("rope_rotate_rows", "fa_decode_combine", "quant_rows_kernel", "col_max_kernel",
+                 "quant_cols_kernel"):
+        assert any(frag in n for n in names), frag
