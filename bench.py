@@ -14,7 +14,8 @@ inputs that is the K pre-rotation kernel plus the attention kernel).
 Prints ONE JSON line:
   value      TFLOP/s of whole steps (exact masked pair count,
              4*B*Hq*pairs*D FLOPs) over the timed steps, HIP events on
-             torch's current stream, which the library launches on;
+             torch's current stream, which the library launches on; the
+             default 50 warmup steps let the GPU clocks reach steady state;
   roofline   the attention kernel alone: FLOPs (or, for decode, algorithmic
              bytes) divided by its mean launch time from the library's kernel
              timer (HIP events recorded around that kernel's launches on its
@@ -234,7 +235,7 @@ def make_step(wl: Workload, dev, host=None):
     raise ValueError(wl.kind)
 
 
-def int8_quantized_e2e(dev, steps: int = 10, warmup: int = 3):
+def int8_quantized_e2e(dev, steps: int = 10, warmup: int = 20):
     """flash_attn_int8qk_quantized on fp16 inputs of the INT8 workload's shape
     (B=2, Hq=32, Hkv=8, S=8192, D=128, causal), timed whole: this library's
     path (three quantiser kernels + the INT8 kernel with the per-channel V
@@ -295,7 +296,10 @@ def int8_quantized_e2e(dev, steps: int = 10, warmup: int = 3):
 
 def time_steps(step, steps: int, warmup: int):
     """Runs `warmup` untimed steps, then `steps` timed ones bracketed by
-    device synchronisation; returns (ms per step, mean kernel ms, launches, wall s)."""
+    device synchronisation (HIP events on torch's stream; no other
+    instrumentation), then the same number again under the library's kernel
+    timer for the kernels' own time.  Returns (ms per step, mean kernel ms,
+    kernel launches, wall s of the timed steps)."""
     import torch
 
     import rdnattention_amd as ra
@@ -306,15 +310,19 @@ def time_steps(step, steps: int, warmup: int):
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(stop) / steps
     with ra.KernelTimer() as kt:
-        t0 = time.perf_counter()
-        start.record(stream)
         for _ in range(steps):
             step()
-        stop.record(stream)
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    return start.elapsed_time(stop) / steps, kt.mean_ms, kt.launches, wall
+    return ms_step, kt.mean_ms, kt.launches, wall
 
 
 def roofline(wl: Workload, kernel_ms: float, traffic):
@@ -479,7 +487,9 @@ def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # GPU clocks ramp up over the first ~20 ms of sustained load: 50 untimed
+    # steps (~35 ms at the default workload) put the timed steps at steady state
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-secondary", action="store_true", help="measure the selected workload only")
@@ -519,7 +529,7 @@ def main(argv=None):
             owl = WORKLOADS[other]
             try:
                 ostep = make_step(owl, dev)
-                oms, okms, _, _ = time_steps(ostep, 10, 3)
+                oms, okms, _, _ = time_steps(ostep, 10, 20)
                 del ostep
                 rf = roofline(owl, okms, profiled_traffic(other, owl))
                 secondary[other] = {"ms_per_step": round(oms, 4), "kernel_ms": round(okms, 4), "roofline": rf}
