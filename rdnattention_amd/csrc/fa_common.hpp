@@ -198,6 +198,27 @@ __device__ __forceinline__ void wg_tile(int wg, int n_hg, int n_rt, int chunk, i
     }
 }
 
+// Work item `k` of persistent workgroup `w` in a grid of `P`, for `n` items
+// numbered like the workgroups of a one-item-per-workgroup grid (which
+// wg_tile places on XCD id % 8); -1 once the workgroup has none left.
+// Workgroups go to the XCDs round-robin, so with P a multiple of 8 workgroup
+// w takes only ids of its own XCD: in rounds of P/8 ids, dealt in alternating
+// (snake) order so that the heaviest and lightest row tiles of a round pair
+// up. Every id < n is taken exactly once (each round's slots map one-to-one
+// onto the XCD's workgroups), and a workgroup's ids increase with k.
+__device__ __forceinline__ int persistent_item(int w, int P, int k, int n) {
+    int id;
+    if ((P & 7) == 0) {
+        const int per_xcd = P >> 3;
+        const int l = w >> 3;
+        const int slot = (k & 1) ? per_xcd - 1 - l : l;
+        id = (w & 7) + 8 * (k * per_xcd + slot);
+    } else {
+        id = w + k * P;
+    }
+    return id < n ? id : -1;
+}
+
 // Raw buffer resource (gfx9 V#: stride 0, DATA_FORMAT 32): loads at byte
 // offsets >= num_records return 0, which is how rows past the end of K/V read
 // as zeros without per-load branches.
@@ -247,9 +268,7 @@ __device__ __forceinline__ uint32_t range_bytes(int64_t rows_left, int64_t strid
 // RoPE on 8 consecutive channels (4 interleaved pairs) of one row:
 // (a, b) -> (a*c - b*s, a*s + b*c) in fp32, rounded to fp16, where c/s are
 // table columns col0 .. col0+3 (src/rdna/fa2_forward_f16.hip:63-77).
-__device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin_row, int col0) {
-    f4 c = *reinterpret_cast<const f4*>(cos_row + col0);
-    f4 s = *reinterpret_cast<const f4*>(sin_row + col0);
+__device__ __forceinline__ h8 rope8_cs(h8 x, f4 c, f4 s) {
     h8 y;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -259,6 +278,42 @@ __device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin
         y[2 * i + 1] = (_Float16)(a * s[i] + b * c[i]);
     }
     return y;
+}
+
+__device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin_row, int col0) {
+    return rope8_cs(x, *reinterpret_cast<const f4*>(cos_row + col0), *reinterpret_cast<const f4*>(sin_row + col0));
+}
+
+// Q^T operand of one query row for the 32x32x16 MFMAs: out[s] = Q[row][16s + 8g .. +7],
+// RoPE-rotated with the table row of this position when `rope`, negated when `neg`, zero
+// when !valid. `qrow`, `cos_row` and `sin_row` must point at readable rows even when
+// !valid. Every load is issued before any is used, so the row costs one memory round
+// trip; with the RoPE loads inside a per-chunk branch the compiler waited for each
+// chunk's loads in turn.
+template <int NS>
+__device__ __forceinline__ void load_q_operand(h8 (&out)[NS], const _Float16* qrow, const float* cos_row,
+                                               const float* sin_row, int g, bool valid, bool rope, bool neg) {
+    h8 x[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        x[s] = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
+    }
+    if (rope) {
+        f4 c[NS], sn[NS];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            c[s] = *reinterpret_cast<const f4*>(cos_row + 8 * s + 4 * g);
+            sn[s] = *reinterpret_cast<const f4*>(sin_row + 8 * s + 4 * g);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            x[s] = rope8_cs(x[s], c[s], sn[s]);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        out[s] = valid ? (neg ? -x[s] : x[s]) : h8{};
+    }
 }
 
 } // namespace rdna_amd

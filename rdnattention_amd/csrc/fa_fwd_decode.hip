@@ -103,21 +103,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa_fwd_f16_decode(DecodeParams
 
     h8 qreg[C::NS];
     {
-        const _Float16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)q * p.q_ss;
-#pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            h8 x = {};
-            if (col_valid) {
-                x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-                if (p.rope_q) {
-                    x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
-                }
-                if (p.q_sign < 0.0f) {
-                    x = -x;
-                }
-            }
-            qreg[s] = x;
-        }
+        const int qr = q; // 0 for an unused column
+        const _Float16* qrow = p.q + b * p.q_sb + h * p.q_sh + (int64_t)qr * p.q_ss;
+        load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, col_valid,
+                       p.rope_q != 0, p.q_sign < 0.0f);
     }
     // Q is in registers before any DMA is issued, so no later wait for it can
     // drain the DMA queue (the compiler does not see the DMAs)

@@ -185,21 +185,10 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     h8 qreg[C::NS];
     {
         const bool valid = q < p.Sq;
-        const _Float16* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
-#pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            h8 x = {};
-            if (valid) {
-                x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-                if (p.rope_q) {
-                    x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
-                }
-                if (p.q_sign < 0.0f) {
-                    x = -x;
-                }
-            }
-            qreg[s] = x;
-        }
+        const int qr = valid ? q : 0;
+        const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
+        load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
+                       p.rope_q != 0, p.q_sign < 0.0f);
     }
 
     // ---- key tiles this workgroup can see
@@ -356,6 +345,11 @@ struct PPCfg {
     static constexpr int KCH = D / 8;
     static constexpr int HALF_TASK = 32 * KCH;         // one group's chunks of one K (or V) tile
     static constexpr int CT = (HALF_TASK + 255) / 256; // K (and V) chunks per thread
+    // One resident workgroup per CU from D = 64 up (VGPRs): a persistent grid
+    // then saves the workgroup switches and balances the row tiles. At D = 32
+    // two workgroups share a CU and hide each other's prologue instead, which
+    // the persistent loop's extra registers would prevent.
+    static constexpr bool PERSIST = D >= 64;
 };
 
 template <int D>
@@ -374,79 +368,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     const int grp = wave >> 2;       // 0 = group A, 1 = group B
     const int gtid = tid & 255;      // thread index inside the group
 
-    const int wg = blockIdx.x;
-    int hg, rt;
-    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
-    const int per_b = p.Hkv * p.groups_per_kv;
-    const int b = hg / per_b;
-    const int rem = hg - b * per_b;
-    const int kvh = rem / p.groups_per_kv;
-    const int sub = rem - kvh * p.groups_per_kv;
-    const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
-    const int wg_q0 = rt * p.rows_per_wg;
-    const int q0 = wg_q0 + (wave / p.G) * 32;
-    const int q = q0 + l32;
-    const bool wave_active = q0 < p.Sq;
-    const int q_hi = min(q0 + 31, p.Sq - 1);
-
-    const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-    const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
-    const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
-    _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
-
-    // Q^T operand (lane holds Q[q][16s + 8g .. +7], RoPE applied); loaded in
-    // the prologue after the first K/V loads are issued so the latencies overlap
-    h8 qreg[C::NS];
-    auto load_q = [&]() {
-        const bool valid = q < p.Sq;
-        const _Float16* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
-#pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            h8 x = {};
-            if (valid) {
-                x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-                if (p.rope_q) {
-                    x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
-                }
-                if (p.q_sign < 0.0f) {
-                    x = -x;
-                }
-            }
-            qreg[s] = x;
-        }
-    };
-
-    const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
-    int klo, khi;
-    visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
-    int t_begin = 0, n = 0;
-    if (khi >= klo) {
-        t_begin = klo / kBN;
-        n = khi / kBN + 1 - t_begin;
-    }
-    const int Sk = p.mask.sk;
-    int row_lo, row_hi;
-    row_key_bounds(p.mask, q, row_lo, row_hi);
-
-    f16x oacc[C::NDT];
-#pragma unroll
-    for (int dt = 0; dt < C::NDT; dt++) {
-        oacc[dt] = f16x{};
-    }
-    float m_run = -INFINITY;
-    float l_run = 0.0f;
-    f16x sacc[2];
-    sacc[0] = f16x{};
-    sacc[1] = f16x{};
-    h8 pb[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        pb[u] = h8{};
-    }
-    int cls_prev = 0; // classification of the tile whose P is held in pb
-
     // ---- staging: this group's half (rows 32*grp .. +31) of K(x) and V(x-1)
-    h8 kreg[C::CT], vreg[C::CT];
     uint32_t coff_k[C::CT], coff_v[C::CT];
     int clk[C::CT], clv[C::CT]; // LDS element offsets inside a tile, -1 = no chunk
 #pragma unroll
@@ -460,236 +382,326 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         clk[it] = ok ? row * C::LDK + 8 * ch : -1;
         clv[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
-    // registers <- HBM for pair x (K tile x if x < n, V tile x-1 if 1 <= x <= n);
-    // a missing tile gets num_records 0, so its loads return 0 and touch nothing
-    auto load_pair = [&](int x) {
-        const int tk = t_begin + x, tv = t_begin + x - 1;
-        const auto rk = make_rsrc(kbase + (int64_t)tk * kBN * p.k_ss,
-                                  x < n ? range_bytes(Sk - tk * kBN, p.k_ss * 2, D * 2) : 0u);
-        const auto rv = make_rsrc(vbase + (int64_t)tv * kBN * p.v_ss,
-                                  (x >= 1 && x <= n) ? range_bytes(Sk - tv * kBN, p.v_ss * 2, D * 2) : 0u);
-#pragma unroll
-        for (int it = 0; it < C::CT; it++) {
-            kreg[it] = buffer_load_h8(rk, coff_k[it], 0);
-            vreg[it] = buffer_load_h8(rv, coff_v[it], 0);
-        }
-    };
-    // LDS <- registers for pair x
-    auto store_pair = [&](int x) {
-        _Float16* sK = sKs + (x & 1) * C::TILE_K;
-        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
-#pragma unroll
-        for (int it = 0; it < C::CT; it++) {
-            if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
-                if (x < n) {
-                    *reinterpret_cast<h8*>(&sK[clk[it]]) = kreg[it];
-                }
-                if (x >= 1 && x <= n) {
-                    *reinterpret_cast<h8*>(&sV[clv[it]]) = vreg[it];
-                }
-            }
-        }
-    };
+    // Persistent (PPCfg::PERSIST): this workgroup walks its share of the row
+    // tiles (one per workgroup of a one-tile-per-workgroup grid, see
+    // persistent_item). Every group passes the same barriers per item and
+    // leaves an item only after its last LDS read, so the next item's
+    // prologue may overwrite LDS. Otherwise the grid has one workgroup per
+    // row tile.
+    auto run_tile = [&](const int wg) {
+        int hg, rt;
+        wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
+        const int per_b = p.Hkv * p.groups_per_kv;
+        const int b = hg / per_b;
+        const int rem = hg - b * per_b;
+        const int kvh = rem / p.groups_per_kv;
+        const int sub = rem - kvh * p.groups_per_kv;
+        const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
+        const int wg_q0 = rt * p.rows_per_wg;
+        const int q0 = wg_q0 + (wave / p.G) * 32;
+        const int q = q0 + l32;
+        const bool wave_active = q0 < p.Sq;
+        const int q_hi = min(q0 + 31, p.Sq - 1);
 
-    // M(i): O += V(i-1)^T P(i-1) (i >= 1) then S(i) = K(i) Q^T (i < n), as one
-    // stream of MFMAs whose LDS operands are read kOpDepth MFMAs ahead through
-    // a small register ring; sched_barrier stops the compiler from hoisting
-    // every read (which would need ~100 more VGPRs).
-    auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
-        constexpr bool DO_PV = decltype(do_pv_c)::value;
-        constexpr bool DO_S = decltype(do_s_c)::value;
-        constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
-        constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
-        constexpr int T = NPV + NSK;
-        constexpr int DEPTH = T < kOpDepth ? T : kOpDepth;
-        const int j16 = lane & 15;
-        const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
-                               16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-        const _Float16* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 8 * g;
-        auto op = [&](int j) -> h8 {
-            if (j < NPV) {
-                const int u = j / C::NDT, dt = j % C::NDT;
-                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-            const int js = j - NPV, st = js >> 1, kt = js & 1;
-            return *reinterpret_cast<const h8*>(krow + kt * 32 * C::LDK + 16 * st);
+        const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
+        const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
+        const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
+        _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
+
+        // Q^T operand (lane holds Q[q][16s + 8g .. +7], RoPE applied); loaded in
+        // the prologue after the first K/V loads are issued so the latencies overlap
+        h8 qreg[C::NS];
+        auto load_q = [&]() {
+            const bool valid = q < p.Sq;
+            const int qr = valid ? q : 0;
+            const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
+            load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
+                           p.rope_q != 0, p.q_sign < 0.0f);
         };
-        f16x acc0 = {}, acc1 = {};
-        h8 ring[DEPTH > 0 ? DEPTH : 1];
-#pragma unroll
-        for (int j = 0; j < DEPTH; j++) {
-            ring[j] = op(j);
+
+        const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
+        int klo, khi;
+        visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
+        int t_begin = 0, n = 0;
+        if (khi >= klo) {
+            t_begin = klo / kBN;
+            n = khi / kBN + 1 - t_begin;
         }
+        const int Sk = p.mask.sk;
+        int row_lo, row_hi;
+        row_key_bounds(p.mask, q, row_lo, row_hi);
+
+        f16x oacc[C::NDT];
 #pragma unroll
-        for (int j = 0; j < T; j++) {
-            const h8 a = ring[j % DEPTH];
-            if (j + DEPTH < T) {
-                ring[j % DEPTH] = op(j + DEPTH);
+        for (int dt = 0; dt < C::NDT; dt++) {
+            oacc[dt] = f16x{};
+        }
+        float m_run = -INFINITY;
+        float l_run = 0.0f;
+        f16x sacc[2];
+        sacc[0] = f16x{};
+        sacc[1] = f16x{};
+        h8 pb[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            pb[u] = h8{};
+        }
+        int cls_prev = 0; // classification of the tile whose P is held in pb
+
+        h8 kreg[C::CT], vreg[C::CT];
+        // registers <- HBM for pair x (K tile x if x < n, V tile x-1 if 1 <= x <= n);
+        // a missing tile gets num_records 0, so its loads return 0 and touch nothing
+        auto load_pair = [&](int x) {
+            const int tk = t_begin + x, tv = t_begin + x - 1;
+            const auto rk = make_rsrc(kbase + (int64_t)tk * kBN * p.k_ss,
+                                      x < n ? range_bytes(Sk - tk * kBN, p.k_ss * 2, D * 2) : 0u);
+            const auto rv = make_rsrc(vbase + (int64_t)tv * kBN * p.v_ss,
+                                      (x >= 1 && x <= n) ? range_bytes(Sk - tv * kBN, p.v_ss * 2, D * 2) : 0u);
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                kreg[it] = buffer_load_h8(rk, coff_k[it], 0);
+                vreg[it] = buffer_load_h8(rv, coff_v[it], 0);
             }
-            if (j < NPV) {
-                const int u = j / C::NDT, dt = j % C::NDT;
-                oacc[dt] = mfma_32x32x16_f16(a, pb[u], oacc[dt]);
-            } else {
-                const int js = j - NPV, st = js >> 1;
-                if (js & 1) {
-                    acc1 = mfma_32x32x16_f16(a, qreg[st], acc1);
-                } else {
-                    acc0 = mfma_32x32x16_f16(a, qreg[st], acc0);
+        };
+        // LDS <- registers for pair x
+        auto store_pair = [&](int x) {
+            _Float16* sK = sKs + (x & 1) * C::TILE_K;
+            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
+                    if (x < n) {
+                        *reinterpret_cast<h8*>(&sK[clk[it]]) = kreg[it];
+                    }
+                    if (x >= 1 && x <= n) {
+                        *reinterpret_cast<h8*>(&sV[clv[it]]) = vreg[it];
+                    }
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (DO_S) {
-            sacc[0] = acc0;
-            sacc[1] = acc1;
-        }
-    };
-    auto phase_m = [&](int i) {
-        if (!wave_active) {
-            return;
-        }
-        const bool do_pv = i >= 1 && cls_prev != 0;
-        int cls_now = 0;
-        if (i < n) {
-            const int kt0 = (t_begin + i) * kBN;
-            cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
-        }
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-        if (do_pv && cls_now != 0) {
-            mfma_stream(T_{}, T_{}, i);
-        } else if (do_pv) {
-            mfma_stream(T_{}, F_{}, i);
-        } else if (cls_now != 0) {
-            mfma_stream(F_{}, T_{}, i);
-        }
-        cls_prev = cls_now;
-    };
+        };
 
-    // V(i): softmax of S(i) -> pb, rescale O
-    auto phase_v = [&](int i) {
-        if (!wave_active || cls_prev == 0) {
-            return;
-        }
-        if (cls_prev == 2) {
-            const int kt0 = (t_begin + i) * kBN;
-            const int a = row_lo - kt0 - 4 * g;
-            const int bnd = row_hi - kt0 - 4 * g;
+        // M(i): O += V(i-1)^T P(i-1) (i >= 1) then S(i) = K(i) Q^T (i < n), as one
+        // stream of MFMAs whose LDS operands are read kOpDepth MFMAs ahead through
+        // a small register ring; sched_barrier stops the compiler from hoisting
+        // every read (which would need ~100 more VGPRs).
+        auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+            constexpr bool DO_PV = decltype(do_pv_c)::value;
+            constexpr bool DO_S = decltype(do_s_c)::value;
+            constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
+            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
+            constexpr int T = NPV + NSK;
+            constexpr int DEPTH = T < kOpDepth ? T : kOpDepth;
+            const int j16 = lane & 15;
+            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
+                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+            const _Float16* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 8 * g;
+            auto op = [&](int j) -> h8 {
+                if (j < NPV) {
+                    const int u = j / C::NDT, dt = j % C::NDT;
+                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                    h4 lo = lds_read_tr16(base);
+                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+                const int js = j - NPV, st = js >> 1, kt = js & 1;
+                return *reinterpret_cast<const h8*>(krow + kt * 32 * C::LDK + 16 * st);
+            };
+            f16x acc0 = {}, acc1 = {};
+            h8 ring[DEPTH > 0 ? DEPTH : 1];
+#pragma unroll
+            for (int j = 0; j < DEPTH; j++) {
+                ring[j] = op(j);
+            }
+#pragma unroll
+            for (int j = 0; j < T; j++) {
+                const h8 a = ring[j % DEPTH];
+                if (j + DEPTH < T) {
+                    ring[j % DEPTH] = op(j + DEPTH);
+                }
+                if (j < NPV) {
+                    const int u = j / C::NDT, dt = j % C::NDT;
+                    oacc[dt] = mfma_32x32x16_f16(a, pb[u], oacc[dt]);
+                } else {
+                    const int js = j - NPV, st = js >> 1;
+                    if (js & 1) {
+                        acc1 = mfma_32x32x16_f16(a, qreg[st], acc1);
+                    } else {
+                        acc0 = mfma_32x32x16_f16(a, qreg[st], acc0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (DO_S) {
+                sacc[0] = acc0;
+                sacc[1] = acc1;
+            }
+        };
+        auto phase_m = [&](int i) {
+            if (!wave_active) {
+                return;
+            }
+            const bool do_pv = i >= 1 && cls_prev != 0;
+            int cls_now = 0;
+            if (i < n) {
+                const int kt0 = (t_begin + i) * kBN;
+                cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
+            }
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (do_pv && cls_now != 0) {
+                mfma_stream(T_{}, T_{}, i);
+            } else if (do_pv) {
+                mfma_stream(T_{}, F_{}, i);
+            } else if (cls_now != 0) {
+                mfma_stream(F_{}, T_{}, i);
+            }
+            cls_prev = cls_now;
+        };
+
+        // V(i): softmax of S(i) -> pb, rescale O
+        auto phase_v = [&](int i) {
+            if (!wave_active || cls_prev == 0) {
+                return;
+            }
+            if (cls_prev == 2) {
+                const int kt0 = (t_begin + i) * kBN;
+                const int a = row_lo - kt0 - 4 * g;
+                const int bnd = row_hi - kt0 - 4 * g;
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
+                        sacc[kt][e] = (off < a || off > bnd) ? -INFINITY : sacc[kt][e];
+                    }
+                }
+            }
+            float mx = sacc[0][0];
+#pragma unroll
+            for (int e = 1; e < 16; e++) {
+                mx = fmaxf(mx, sacc[0][e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                mx = fmaxf(mx, sacc[1][e]);
+            }
+            mx = pair_max(mx);
+            const float m_new = fmaxf(m_run, mx * p.c);
+            const bool grow = m_new > m_run + kRescaleThreshold;
+            if (wave_any(grow)) {
+                const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+                if (grow) {
+                    m_run = m_new;
+                }
+                l_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < C::NDT; dt++) {
+                    oacc[dt] *= alpha;
+                }
+            }
+            const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+            float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
-                    sacc[kt][e] = (off < a || off > bnd) ? -INFINITY : sacc[kt][e];
+                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                psum = sum_h8(pb[u], psum);
+            }
+            l_run += psum;
+        };
+
+        // ---- prologue: pair 0 in LDS; each group's registers hold its next pair
+        if (n > 0) {
+            load_pair(0);
+        }
+        load_q();
+        if (n > 0) {
+            store_pair(0);
+            load_pair(1);
+        }
+        __syncthreads();
+        // Both groups pass 2n + 2 barriers; group B starts one phase late.
+        if (n > 0) {
+            if (grp == 0) {
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 1);
+                    load_pair(i + 2);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+                __syncthreads();
+            } else {
+                store_pair(1);
+                load_pair(2);
+                __syncthreads();
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 2);
+                    load_pair(i + 3);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+            }
+        }
+
+        if (!wave_active) {
+            return;
+        }
+        const float l = pair_sum(l_run);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        if (q < p.Sq) {
+            _Float16* orow = obase + (int64_t)q * p.o_ss;
+#pragma unroll
+            for (int dt = 0; dt < C::NDT; dt++) {
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
+                             (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
+                    *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
                 }
             }
         }
-        float mx = sacc[0][0];
-#pragma unroll
-        for (int e = 1; e < 16; e++) {
-            mx = fmaxf(mx, sacc[0][e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            mx = fmaxf(mx, sacc[1][e]);
-        }
-        mx = pair_max(mx);
-        const float m_new = fmaxf(m_run, mx * p.c);
-        const bool grow = m_new > m_run + kRescaleThreshold;
-        if (wave_any(grow)) {
-            const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
-            if (grow) {
-                m_run = m_new;
-            }
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-                oacc[dt] *= alpha;
-            }
-        }
-        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
-        float psum = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            psum = sum_h8(pb[u], psum);
-        }
-        l_run += psum;
     };
-
-    // ---- prologue: pair 0 in LDS; each group's registers hold its next pair
-    if (n > 0) {
-        load_pair(0);
-    }
-    load_q();
-    if (n > 0) {
-        store_pair(0);
-        load_pair(1);
-    }
-    __syncthreads();
-    // Both groups pass 2n + 2 barriers; group B starts one phase late.
-    if (n > 0) {
-        if (grp == 0) {
-            for (int i = 0; i < n; i++) {
-                phase_m(i);
-                __syncthreads();
-                store_pair(i + 1);
-                load_pair(i + 2);
-                phase_v(i);
-                __syncthreads();
+    if constexpr (C::PERSIST) {
+        for (int item = 0;; item++) {
+            const int wg = persistent_item(blockIdx.x, gridDim.x, item, p.n_items);
+            if (wg < 0) {
+                break;
             }
-            phase_m(n);
-            __syncthreads();
-            __syncthreads();
-        } else {
-            store_pair(1);
-            load_pair(2);
-            __syncthreads();
-            for (int i = 0; i < n; i++) {
-                phase_m(i);
-                __syncthreads();
-                store_pair(i + 2);
-                load_pair(i + 3);
-                phase_v(i);
-                __syncthreads();
-            }
-            phase_m(n);
-            __syncthreads();
+            run_tile(wg);
         }
-    }
-
-    if (!wave_active) {
-        return;
-    }
-    const float l = pair_sum(l_run);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (q < p.Sq) {
-        _Float16* orow = obase + (int64_t)q * p.o_ss;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
-                         (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
-                *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
-            }
-        }
+    } else {
+        run_tile(blockIdx.x);
     }
 }
 
 template <int D>
 int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    // persistent: as many workgroups as the device holds at once, each
+    // walking its share of the n_wg row tiles
+    int64_t grid = n_wg;
+    if (PPCfg<D>::PERSIST) {
+        const int64_t resident =
+            resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_f16_pp<D>), kPPThreads, err);
+        if (resident <= 0) {
+            return -1;
+        }
+        grid = std::min(n_wg, resident);
+    }
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_f16_pp<D>, dim3((uint32_t)n_wg), dim3(kPPThreads), 0, stream, p);
+    hipLaunchKernelGGL(fa_fwd_f16_pp<D>, dim3((uint32_t)grid), dim3(kPPThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -768,6 +780,7 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.rope_q = rope_q ? 1 : 0;
 
     const int64_t n_wg = (int64_t)p.n_row_tiles * p.n_head_groups;
+    p.n_items = (int32_t)std::min<int64_t>(n_wg, INT32_MAX);
     if (n_wg <= 0) {
         err = "empty launch grid";
         return -1;

@@ -207,21 +207,10 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
     h8 qreg[C::NS];
     {
         const bool valid = q < p.Sq;
-        const _Float16* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
-#pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            h8 x = {};
-            if (valid) {
-                x = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-                if (p.rope_q) {
-                    x = rope8(x, p.rot_cos + (int64_t)q * (D / 2), p.rot_sin + (int64_t)q * (D / 2), 8 * s + 4 * g);
-                }
-                if (p.q_sign < 0.0f) {
-                    x = -x;
-                }
-            }
-            qreg[s] = x;
-        }
+        const int qr = valid ? q : 0;
+        const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
+        load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
+                       p.rope_q != 0, p.q_sign < 0.0f);
     }
     // Q is in registers before the first DMA, so the per-tile vmcnt waits
     // below only ever wait for DMAs (the compiler does not see those)

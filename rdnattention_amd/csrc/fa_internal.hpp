@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <cstdint>
 #include <string>
 
 namespace rdna_amd {
@@ -43,6 +44,11 @@ class KernelTimerGuard {
     hipStream_t stream_;
     hipEvent_t start_ = nullptr;
 };
+
+// Workgroups of `kernel` (launched with `threads` threads and no dynamic LDS)
+// that the current device holds at once: compute units x workgroups per
+// compute unit. Cached per device and kernel; <= 0 with `err` set on failure.
+int64_t resident_workgroups(const void* kernel, int threads, std::string& err);
 
 // Launchers.
 int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err);

@@ -28,6 +28,7 @@ struct PrefillParams {
     int32_t n_head_groups; // B * Hkv * groups_per_kv
     int32_t groups_per_kv; // ratio / G
     int32_t hg_chunk;      // head groups per XCD at a time (0 = head groups fastest)
+    int32_t n_items;       // n_row_tiles * n_head_groups (persistent kernels)
     float c;               // max(|scale| * log2(e), 1e-30)
     float q_sign;          // sign of scale, folded into Q (exact in fp16)
     MaskSpec mask;

@@ -11,6 +11,10 @@
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
 
+#include <cstdint>
+#include <map>
+#include <mutex>
+
 namespace rdna_amd {
 namespace {
 
@@ -37,12 +41,62 @@ __global__ __launch_bounds__(256) void rope_rotate_rows(const _Float16* __restri
 
 } // namespace
 
+namespace {
+
+constexpr uint64_t kScratchRetain = 4ull << 30;
+
+// One memory pool per device for the scratch buffers, created on first use.
+// Its release threshold keeps up to kScratchRetain bytes of freed blocks in
+// the pool instead of returning them to the device at each synchronisation,
+// so the per-call hipMallocFromPoolAsync / hipFreeAsync pair reuses memory
+// rather than mapping it anew (which left the GPU idle between kernels).
+int scratch_pool(hipMemPool_t& pool, std::string& err) {
+    static std::mutex mu;
+    static std::map<int, hipMemPool_t> pools; // guarded by mu
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        err = std::string("scratch pool: ") + hipGetErrorString(e);
+        return -1;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = pools.find(dev);
+    if (it != pools.end()) {
+        pool = it->second;
+        return 0;
+    }
+    hipMemPoolProps props = {};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    e = hipMemPoolCreate(&pool, &props);
+    if (e == hipSuccess) {
+        uint64_t keep = kScratchRetain;
+        e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) {
+            (void)hipMemPoolDestroy(pool);
+        }
+    }
+    if (e != hipSuccess) {
+        err = std::string("scratch pool: ") + hipGetErrorString(e);
+        return -1;
+    }
+    pools[dev] = pool;
+    return 0;
+}
+
+} // namespace
+
 int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
     stream = s;
     if (bytes == 0) {
         return 0;
     }
-    hipError_t e = hipMallocAsync(&ptr, bytes, s);
+    hipMemPool_t pool = nullptr;
+    if (scratch_pool(pool, err) != 0) {
+        return -1;
+    }
+    hipError_t e = hipMallocFromPoolAsync(&ptr, bytes, pool, s);
     if (e != hipSuccess) {
         ptr = nullptr;
         err = std::string("scratch allocation failed: ") + hipGetErrorString(e);

@@ -307,3 +307,35 @@ def test_late_score_spike(gpu, oracle_lib, d, jump, causal):
     torch.cuda.synchronize()
     ref = reference_f16(q, k, v, causal, -1)
     assert_f16_parity(out.float().cpu().numpy(), ref, f"spike d{d} jump{jump}")
+
+
+# Row-tile work items well beyond what the device holds at once (at most 512
+# workgroups of these kernels on 256 CUs), so every persistent workgroup walks
+# several items, with ragged sequence ends and items of unequal size.
+# name, b, hq, hkv, s, d, causal, window, rope
+PERSISTENT_CASES = [
+    ("d128_gqa4_causal_rope", 4, 32, 8, 1100, 128, True, -1, True),     # 32 head groups x 18 row tiles
+    ("d96_gqa4_causal_window", 4, 32, 8, 1500, 96, True, 200, False),   # 32 x 24
+    ("d64_mha_window", 2, 16, 16, 3000, 64, False, 500, False),         # 32 x 12
+    ("d32_gqa2_dense", 4, 16, 8, 2100, 32, False, -1, False),           # 32 x 17
+    ("d128_mqa_causal", 1, 16, 1, 2500, 128, True, -1, True),           # 4 x 40
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=[c[0] for c in PERSISTENT_CASES])
+def test_persistent_workgroups_cover_every_tile(gpu, oracle_lib, case):
+    """Output pre-filled with NaN: a row tile that no workgroup writes fails
+    the finiteness check, one written wrongly fails the FP16 bar."""
+    name, b, hq, hkv, s, d, causal, window, rope = case
+    log(f"[persistent] {name}")
+    q, k, v = seeded_inputs(21, b, hq, hkv, s, s, d)
+    cos = sin = None
+    if rope:
+        cos, sin = oracle.rope_tables(s, d)
+    out = torch.full_like(q, float("nan"), device=gpu)
+    rc = forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal, window,
+                     torch.from_numpy(cos).to(gpu) if rope else None,
+                     torch.from_numpy(sin).to(gpu) if rope else None, path=1)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert_f16_parity(out.float().cpu().numpy(), reference_f16(q, k, v, causal, window, cos, sin), name)
