@@ -345,6 +345,10 @@ struct PPCfg {
     static constexpr int KCH = D / 8;
     static constexpr int HALF_TASK = 32 * KCH;         // one group's chunks of one K (or V) tile
     static constexpr int CT = (HALF_TASK + 255) / 256; // K (and V) chunks per thread
+    // Q of the row tile, RoPE applied: [wave][32 rows][LDQ], read like K rows
+    static constexpr int LDQ = D + 8;
+    static constexpr int TILE_Q = kPPWaves * 32 * LDQ;
+    static constexpr int QCT = kPPWaves * 32 * KCH / kPPThreads; // Q chunks per thread (= NS)
     // One resident workgroup per CU from D = 64 up (VGPRs): a persistent grid
     // then saves the workgroup switches and balances the row tiles. At D = 32
     // two workgroups share a CU and hide each other's prologue instead, which
@@ -355,10 +359,11 @@ struct PPCfg {
 template <int D>
 __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) {
     using C = PPCfg<D>;
-    // sK[slot], sV[slot]
-    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::TILE_K + 2 * C::TILE_V];
+    // sK[slot], sV[slot], sQ
+    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::TILE_K + 2 * C::TILE_V + C::TILE_Q];
     _Float16* const sKs = smem;
     _Float16* const sVs = smem + 2 * C::TILE_K;
+    _Float16* const sQ = smem + 2 * C::TILE_K + 2 * C::TILE_V;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -408,15 +413,58 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
         _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
 
-        // Q^T operand (lane holds Q[q][16s + 8g .. +7], RoPE applied); loaded in
-        // the prologue after the first K/V loads are issued so the latencies overlap
+        // Q^T operand (lane holds Q[q][16s + 8g .. +7], RoPE applied), staged
+        // through sQ: in the operand layout each lane reads 16 B of its own row,
+        // so every load instruction touches 32 rows (cache lines) and the
+        // prologue waited on L1 lookups. All threads instead load the tile's Q
+        // (and RoPE table) chunks row-contiguously, 16 lanes per 256 B, rotate
+        // them and write sQ; after the prologue barrier each wave reads its
+        // operand from sQ with conflict-free b128 reads (the K-row layout).
         h8 qreg[C::NS];
-        auto load_q = [&]() {
-            const bool valid = q < p.Sq;
-            const int qr = valid ? q : 0;
-            const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
-            load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
-                           p.rope_q != 0, p.q_sign < 0.0f);
+        auto stage_q = [&]() {
+            const _Float16* qb = p.q + b * p.q_sb + (int64_t)(kvh * p.ratio + sub * p.G) * p.q_sh;
+            h8 x[C::QCT];
+            int row[C::QCT], col[C::QCT], dst[C::QCT];
+            bool ok[C::QCT];
+#pragma unroll
+            for (int c = 0; c < C::QCT; c++) {
+                // chunk index over (head j, row r, 16-byte column ch), ch fastest;
+                // row r of head j is row r % 32 of wave j + G * (r / 32)
+                const int idx = tid + kPPThreads * c;
+                const int ch = idx % C::KCH;
+                const int rj = idx / C::KCH;
+                const int j = rj / p.rows_per_wg;
+                const int r = rj - j * p.rows_per_wg;
+                ok[c] = wg_q0 + r < p.Sq;
+                row[c] = ok[c] ? wg_q0 + r : 0;
+                col[c] = ch;
+                dst[c] = ((j + p.G * (r >> 5)) * 32 + (r & 31)) * C::LDQ + 8 * ch;
+                x[c] = *reinterpret_cast<const h8*>(qb + j * p.q_sh + (int64_t)row[c] * p.q_ss + 8 * ch);
+            }
+            if (p.rope_q) {
+                f4 cs[C::QCT], sn[C::QCT];
+#pragma unroll
+                for (int c = 0; c < C::QCT; c++) {
+                    cs[c] = *reinterpret_cast<const f4*>(p.rot_cos + (int64_t)row[c] * (D / 2) + 4 * col[c]);
+                    sn[c] = *reinterpret_cast<const f4*>(p.rot_sin + (int64_t)row[c] * (D / 2) + 4 * col[c]);
+                }
+#pragma unroll
+                for (int c = 0; c < C::QCT; c++) {
+                    x[c] = rope8_cs(x[c], cs[c], sn[c]);
+                }
+            }
+            const bool neg = p.q_sign < 0.0f;
+#pragma unroll
+            for (int c = 0; c < C::QCT; c++) {
+                *reinterpret_cast<h8*>(&sQ[dst[c]]) = ok[c] ? (neg ? -x[c] : x[c]) : h8{};
+            }
+        };
+        auto read_q = [&]() {
+            const _Float16* src = sQ + (wave * 32 + l32) * C::LDQ + 8 * g;
+#pragma unroll
+            for (int st = 0; st < C::NS; st++) {
+                qreg[st] = *reinterpret_cast<const h8*>(src + 16 * st);
+            }
         };
 
         const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
@@ -619,12 +667,13 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         if (n > 0) {
             load_pair(0);
         }
-        load_q();
+        stage_q();
         if (n > 0) {
             store_pair(0);
             load_pair(1);
         }
         __syncthreads();
+        read_q();
         // Both groups pass 2n + 2 barriers; group B starts one phase late.
         if (n > 0) {
             if (grp == 0) {
