@@ -423,30 +423,36 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         h8 qreg[C::NS];
         auto stage_q = [&]() {
             const _Float16* qb = p.q + b * p.q_sb + (int64_t)(kvh * p.ratio + sub * p.G) * p.q_sh;
-            h8 x[C::QCT];
-            int row[C::QCT], col[C::QCT], dst[C::QCT];
-            bool ok[C::QCT];
-#pragma unroll
-            for (int c = 0; c < C::QCT; c++) {
-                // chunk index over (head j, row r, 16-byte column ch), ch fastest;
-                // row r of head j is row r % 32 of wave j + G * (r / 32)
-                const int idx = tid + kPPThreads * c;
-                const int ch = idx % C::KCH;
+            // chunk c of this thread: (head j, row r, 16-byte column ch), ch
+            // fastest; row r of head j is row r % 32 of wave j + G * (r / 32).
+            // Recomputed from an opaque copy of the thread id at each use so
+            // that no index stays live across the loads' latency.
+            struct Chunk {
+                int j, r, ch;
+            };
+            auto chunk = [&](int t, int c) {
+                const int idx = t + kPPThreads * c;
                 const int rj = idx / C::KCH;
                 const int j = rj / p.rows_per_wg;
-                const int r = rj - j * p.rows_per_wg;
-                ok[c] = wg_q0 + r < p.Sq;
-                row[c] = ok[c] ? wg_q0 + r : 0;
-                col[c] = ch;
-                dst[c] = ((j + p.G * (r >> 5)) * 32 + (r & 31)) * C::LDQ + 8 * ch;
-                x[c] = *reinterpret_cast<const h8*>(qb + j * p.q_sh + (int64_t)row[c] * p.q_ss + 8 * ch);
+                return Chunk{j, rj - j * p.rows_per_wg, idx % C::KCH};
+            };
+            auto src_row = [&](const Chunk& k) { return wg_q0 + k.r < p.Sq ? wg_q0 + k.r : 0; };
+            h8 x[C::QCT];
+            int t = tid;
+            asm volatile("" : "+v"(t));
+#pragma unroll
+            for (int c = 0; c < C::QCT; c++) {
+                const Chunk k = chunk(t, c);
+                x[c] = *reinterpret_cast<const h8*>(qb + k.j * p.q_sh + (int64_t)src_row(k) * p.q_ss + 8 * k.ch);
             }
             if (p.rope_q) {
                 f4 cs[C::QCT], sn[C::QCT];
 #pragma unroll
                 for (int c = 0; c < C::QCT; c++) {
-                    cs[c] = *reinterpret_cast<const f4*>(p.rot_cos + (int64_t)row[c] * (D / 2) + 4 * col[c]);
-                    sn[c] = *reinterpret_cast<const f4*>(p.rot_sin + (int64_t)row[c] * (D / 2) + 4 * col[c]);
+                    const Chunk k = chunk(t, c);
+                    const int64_t off = (int64_t)src_row(k) * (D / 2) + 4 * k.ch;
+                    cs[c] = *reinterpret_cast<const f4*>(p.rot_cos + off);
+                    sn[c] = *reinterpret_cast<const f4*>(p.rot_sin + off);
                 }
 #pragma unroll
                 for (int c = 0; c < C::QCT; c++) {
@@ -454,9 +460,12 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 }
             }
             const bool neg = p.q_sign < 0.0f;
+            asm volatile("" : "+v"(t));
 #pragma unroll
             for (int c = 0; c < C::QCT; c++) {
-                *reinterpret_cast<h8*>(&sQ[dst[c]]) = ok[c] ? (neg ? -x[c] : x[c]) : h8{};
+                const Chunk k = chunk(t, c);
+                const int dst = ((k.j + p.G * (k.r >> 5)) * 32 + (k.r & 31)) * C::LDQ + 8 * k.ch;
+                *reinterpret_cast<h8*>(&sQ[dst]) = wg_q0 + k.r < p.Sq ? (neg ? -x[c] : x[c]) : h8{};
             }
         };
         auto read_q = [&]() {
