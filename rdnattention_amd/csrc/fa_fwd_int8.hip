@@ -66,6 +66,7 @@ struct Int8Params {
     int64_t o_sb, o_sh, o_ss;
     int32_t Hq, Sq, Hkv, ratio, G, rows_per_wg, n_row_tiles, n_head_groups, groups_per_kv;
     int32_t hg_chunk; // head groups per XCD at a time (0 = head groups fastest)
+    int32_t n_items;  // n_row_tiles * n_head_groups
     MaskSpec mask;
 };
 
@@ -83,6 +84,7 @@ struct I8Cfg {
     static constexpr int KCH = D / 16;         // 16-byte int8 chunks per row
     static constexpr int HALF_TASK = 32 * KCH; // one group's chunks of one K (or V) tile
     static constexpr int CT = (HALF_TASK + 255) / 256;
+    static constexpr int LDO = D + 8; // halves; output staging rows (conflict-free like K rows)
 };
 
 constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
@@ -122,6 +124,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
     __shared__ __attribute__((aligned(16))) _Float16 sVs[2 * C::TILE_V];
     __shared__ __attribute__((aligned(16))) float sks[2][kI8BN];
+    __shared__ __attribute__((aligned(16))) _Float16 sO[kI8Waves * 32 * C::LDO];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -131,326 +134,335 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     const int grp = wave >> 2;
     const int gtid = tid & 255;
 
-    const int wg = blockIdx.x;
-    int hg, rt;
-    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
-    const int per_b = p.Hkv * p.groups_per_kv;
-    const int b = hg / per_b;
-    const int rem = hg - b * per_b;
-    const int kvh = rem / p.groups_per_kv;
-    const int sub = rem - kvh * p.groups_per_kv;
-    const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
-    const int wg_q0 = rt * p.rows_per_wg;
-    const int q0 = wg_q0 + (wave / p.G) * 32;
-    const int q = q0 + l32;
-    const bool wave_active = q0 < p.Sq;
-    const int q_hi = min(q0 + 31, p.Sq - 1);
-    const int Sk = p.mask.sk;
+    // Persistent: this workgroup walks its share of the row tiles (one per
+    // workgroup of a one-tile-per-workgroup grid, see persistent_item). Every
+    // group passes the same barriers per tile and leaves a tile only after its
+    // last LDS read of K/V, so the next tile's prologue may overwrite them;
+    // each wave's sO slot is its own.
+    auto run_tile = [&](const int wg) {
+        int hg, rt;
+        wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
+        const int per_b = p.Hkv * p.groups_per_kv;
+        const int b = hg / per_b;
+        const int rem = hg - b * per_b;
+        const int kvh = rem / p.groups_per_kv;
+        const int sub = rem - kvh * p.groups_per_kv;
+        const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
+        const int wg_q0 = rt * p.rows_per_wg;
+        const int q0 = wg_q0 + (wave / p.G) * 32;
+        const int q = q0 + l32;
+        const bool wave_active = q0 < p.Sq;
+        const int q_hi = min(q0 + 31, p.Sq - 1);
+        const int Sk = p.mask.sk;
 
-    const int8_t* qbase = p.q + b * p.q_sb + h * p.q_sh;
-    const int8_t* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
-    const int8_t* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
-    _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
-    const float* ksbase = p.ksv ? p.ksv + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
+        const int8_t* qbase = p.q + b * p.q_sb + h * p.q_sh;
+        const int8_t* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
+        const int8_t* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
+        _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
+        const float* ksbase = p.ksv ? p.ksv + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
 
-    // Q^T operand: lane holds Q[q][32s + 16g .. +15]
-    i4 qreg[C::NS];
-    float qs = p.q_scale;
-    {
-        const bool valid = q < p.Sq;
-        const int8_t* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
+        // Q^T operand: lane holds Q[q][32s + 16g .. +15]
+        i4 qreg[C::NS];
+        float qs = p.q_scale;
+        {
+            const bool valid = q < p.Sq;
+            const int8_t* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
 #pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            qreg[s] = valid ? *reinterpret_cast<const i4*>(qrow + 32 * s + 16 * g) : i4{};
-        }
-        if (p.qsv != nullptr && valid) {
-            qs = p.qsv[((int64_t)b * p.Hq + h) * p.Sq + q];
-        }
-    }
-    // s_j = t_j * qc with t_j = S_j * ks_j.  When every lane's qc is positive
-    // the row max is taken over t (one multiply per score saved); otherwise t
-    // is first scaled by qc in place and qeff = 1.
-    const float qc = qs * p.scale_log2e;
-    const bool qpos = !wave_any(!(qc > 0.0f));
-    const float qeff = qpos ? qc : 1.0f;
-
-    const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
-    int klo, khi;
-    visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
-    int t_begin = 0, n = 0;
-    if (khi >= klo) {
-        t_begin = klo / kI8BN;
-        n = khi / kI8BN + 1 - t_begin;
-    }
-    int row_lo, row_hi;
-    row_key_bounds(p.mask, q, row_lo, row_hi);
-
-    f16x oacc[C::NDT];
-#pragma unroll
-    for (int dt = 0; dt < C::NDT; dt++) {
-        oacc[dt] = f16x{};
-    }
-    float m_run = -INFINITY, l_run = 0.0f;
-    f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
-    tsc[0] = f16x{};
-    tsc[1] = f16x{};
-    h8 pb[4]; // P^T operands of the four 16-key groups: integers 0..127 in fp16
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        pb[u] = h8{};
-    }
-    int cls_prev = 0;
-
-    // ---- staging (one group's 32 rows of K and V per pair; ks by group A)
-    i4 kreg[C::CT], vreg[C::CT];
-    uint32_t coff_k[C::CT], coff_v[C::CT];
-    int clk[C::CT], clv[C::CT];
-#pragma unroll
-    for (int it = 0; it < C::CT; it++) {
-        const int e = gtid + it * 256;
-        const bool ok = C::HALF_TASK % 256 == 0 || e < C::HALF_TASK;
-        const int row = 32 * grp + (ok ? e / C::KCH : 0);
-        const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
-        coff_k[it] = (uint32_t)((int64_t)row * p.k_ss + 16 * ch);
-        coff_v[it] = (uint32_t)((int64_t)row * p.v_ss + 16 * ch);
-        clk[it] = ok ? row * C::LDK + 16 * ch : -1;
-        clv[it] = ok ? row * C::LDV + 16 * ch : -1;
-    }
-    float ksreg = 0.0f;
-    auto load_pair = [&](int x) {
-        const int tk = t_begin + x, tv = t_begin + x - 1;
-        const auto rk = make_rsrc(kbase + (int64_t)tk * kI8BN * p.k_ss,
-                                  x < n ? range_bytes(Sk - tk * kI8BN, p.k_ss, D) : 0u);
-        const auto rv = make_rsrc(vbase + (int64_t)tv * kI8BN * p.v_ss,
-                                  (x >= 1 && x <= n) ? range_bytes(Sk - tv * kI8BN, p.v_ss, D) : 0u);
-#pragma unroll
-        for (int it = 0; it < C::CT; it++) {
-            kreg[it] = buffer_load_i4(rk, coff_k[it]);
-            vreg[it] = buffer_load_i4(rv, coff_v[it]);
-        }
-        if (grp == 0 && gtid < kI8BN && x < n) {
-            const int key = tk * kI8BN + gtid;
-            ksreg = (ksbase != nullptr && key < Sk) ? ksbase[key] : p.k_scale;
-        }
-    };
-    auto store_pair = [&](int x) {
-        int8_t* sK = sKs + (x & 1) * C::TILE_K;
-        _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
-#pragma unroll
-        for (int it = 0; it < C::CT; it++) {
-            if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
-                if (x < n) {
-                    *reinterpret_cast<i4*>(&sK[clk[it]]) = kreg[it];
-                }
-                if (x >= 1 && x <= n) {
-                    h8 lo, hi;
-                    i8x16_to_h8x2(vreg[it], lo, hi);
-                    *reinterpret_cast<h8*>(&sV[clv[it]]) = lo;
-                    *reinterpret_cast<h8*>(&sV[clv[it] + 8]) = hi;
-                }
+            for (int s = 0; s < C::NS; s++) {
+                qreg[s] = valid ? *reinterpret_cast<const i4*>(qrow + 32 * s + 16 * g) : i4{};
+            }
+            if (p.qsv != nullptr && valid) {
+                qs = p.qsv[((int64_t)b * p.Hq + h) * p.Sq + q];
             }
         }
-        if (grp == 0 && gtid < kI8BN && x < n) {
-            sks[x & 1][gtid] = ksreg;
-        }
-    };
+        // s_j = t_j * qc with t_j = S_j * ks_j.  When every lane's qc is positive
+        // the row max is taken over t (one multiply per score saved); otherwise t
+        // is first scaled by qc in place and qeff = 1.
+        const float qc = qs * p.scale_log2e;
+        const bool qpos = !wave_any(!(qc > 0.0f));
+        const float qeff = qpos ? qc : 1.0f;
 
-    // M(i): O^T += V(i-1)^T P(i-1)^T (fp16 MFMA, i >= 1) then S(i)^T = K(i) Q^T
-    // (int8 MFMA, i < n): one stream of MFMAs whose LDS operands are read
-    // kI8OpDepth MFMAs ahead through a register ring
-    auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
-        constexpr bool DO_PV = decltype(do_pv_c)::value;
-        constexpr bool DO_S = decltype(do_s_c)::value;
-        constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
-        constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
-        constexpr int T = NPV + NSK;
-        constexpr int DEPTH = T < kI8OpDepth ? T : kI8OpDepth;
-        const int j16 = lane & 15;
-        const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
-                               16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-        const int8_t* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 16 * g;
-        auto op = [&](int j) -> i4 {
-            if (j < NPV) {
-                const int u = j / C::NDT, dt = j % C::NDT;
-                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
+        int klo, khi;
+        visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
+        int t_begin = 0, n = 0;
+        if (khi >= klo) {
+            t_begin = klo / kI8BN;
+            n = khi / kI8BN + 1 - t_begin;
+        }
+        int row_lo, row_hi;
+        row_key_bounds(p.mask, q, row_lo, row_hi);
+
+        f16x oacc[C::NDT];
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; dt++) {
+            oacc[dt] = f16x{};
+        }
+        float m_run = -INFINITY, l_run = 0.0f;
+        f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
+        tsc[0] = f16x{};
+        tsc[1] = f16x{};
+        h8 pb[4]; // P^T operands of the four 16-key groups: integers 0..127 in fp16
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            pb[u] = h8{};
+        }
+        int cls_prev = 0;
+
+        // ---- staging (one group's 32 rows of K and V per pair; ks by group A)
+        i4 kreg[C::CT], vreg[C::CT];
+        uint32_t coff_k[C::CT], coff_v[C::CT];
+        int clk[C::CT], clv[C::CT];
+#pragma unroll
+        for (int it = 0; it < C::CT; it++) {
+            const int e = gtid + it * 256;
+            const bool ok = C::HALF_TASK % 256 == 0 || e < C::HALF_TASK;
+            const int row = 32 * grp + (ok ? e / C::KCH : 0);
+            const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
+            coff_k[it] = (uint32_t)((int64_t)row * p.k_ss + 16 * ch);
+            coff_v[it] = (uint32_t)((int64_t)row * p.v_ss + 16 * ch);
+            clk[it] = ok ? row * C::LDK + 16 * ch : -1;
+            clv[it] = ok ? row * C::LDV + 16 * ch : -1;
+        }
+        float ksreg = 0.0f;
+        auto load_pair = [&](int x) {
+            const int tk = t_begin + x, tv = t_begin + x - 1;
+            const auto rk = make_rsrc(kbase + (int64_t)tk * kI8BN * p.k_ss,
+                                      x < n ? range_bytes(Sk - tk * kI8BN, p.k_ss, D) : 0u);
+            const auto rv = make_rsrc(vbase + (int64_t)tv * kI8BN * p.v_ss,
+                                      (x >= 1 && x <= n) ? range_bytes(Sk - tv * kI8BN, p.v_ss, D) : 0u);
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                kreg[it] = buffer_load_i4(rk, coff_k[it]);
+                vreg[it] = buffer_load_i4(rv, coff_v[it]);
             }
-            const int js = j - NPV, st = js >> 1, kt = js & 1;
-            return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
+            if (grp == 0 && gtid < kI8BN && x < n) {
+                const int key = tk * kI8BN + gtid;
+                ksreg = (ksbase != nullptr && key < Sk) ? ksbase[key] : p.k_scale;
+            }
         };
-        i16x acc0 = {}, acc1 = {};
-        i4 ring[DEPTH > 0 ? DEPTH : 1];
+        auto store_pair = [&](int x) {
+            int8_t* sK = sKs + (x & 1) * C::TILE_K;
+            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
 #pragma unroll
-        for (int j = 0; j < DEPTH; j++) {
-            ring[j] = op(j);
-        }
-#pragma unroll
-        for (int j = 0; j < T; j++) {
-            const i4 a = ring[j % DEPTH];
-            if (j + DEPTH < T) {
-                ring[j % DEPTH] = op(j + DEPTH);
+            for (int it = 0; it < C::CT; it++) {
+                if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
+                    if (x < n) {
+                        *reinterpret_cast<i4*>(&sK[clk[it]]) = kreg[it];
+                    }
+                    if (x >= 1 && x <= n) {
+                        h8 lo, hi;
+                        i8x16_to_h8x2(vreg[it], lo, hi);
+                        *reinterpret_cast<h8*>(&sV[clv[it]]) = lo;
+                        *reinterpret_cast<h8*>(&sV[clv[it] + 8]) = hi;
+                    }
+                }
             }
-            if (j < NPV) {
-                const int u = j / C::NDT, dt = j % C::NDT;
-                oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
-            } else {
-                const int js = j - NPV, st = js >> 1;
-                if (js & 1) {
-                    acc1 = mfma_32x32x32_i8(a, qreg[st], acc1);
+            if (grp == 0 && gtid < kI8BN && x < n) {
+                sks[x & 1][gtid] = ksreg;
+            }
+        };
+
+        // M(i): O^T += V(i-1)^T P(i-1)^T (fp16 MFMA, i >= 1) then S(i)^T = K(i) Q^T
+        // (int8 MFMA, i < n): one stream of MFMAs whose LDS operands are read
+        // kI8OpDepth MFMAs ahead through a register ring
+        auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+            constexpr bool DO_PV = decltype(do_pv_c)::value;
+            constexpr bool DO_S = decltype(do_s_c)::value;
+            constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
+            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
+            constexpr int T = NPV + NSK;
+            constexpr int DEPTH = T < kI8OpDepth ? T : kI8OpDepth;
+            const int j16 = lane & 15;
+            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
+                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+            const int8_t* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 16 * g;
+            auto op = [&](int j) -> i4 {
+                if (j < NPV) {
+                    const int u = j / C::NDT, dt = j % C::NDT;
+                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                    h4 lo = lds_read_tr16(base);
+                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                    return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                }
+                const int js = j - NPV, st = js >> 1, kt = js & 1;
+                return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
+            };
+            i16x acc0 = {}, acc1 = {};
+            i4 ring[DEPTH > 0 ? DEPTH : 1];
+#pragma unroll
+            for (int j = 0; j < DEPTH; j++) {
+                ring[j] = op(j);
+            }
+#pragma unroll
+            for (int j = 0; j < T; j++) {
+                const i4 a = ring[j % DEPTH];
+                if (j + DEPTH < T) {
+                    ring[j % DEPTH] = op(j + DEPTH);
+                }
+                if (j < NPV) {
+                    const int u = j / C::NDT, dt = j % C::NDT;
+                    oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
                 } else {
-                    acc0 = mfma_32x32x32_i8(a, qreg[st], acc0);
+                    const int js = j - NPV, st = js >> 1;
+                    if (js & 1) {
+                        acc1 = mfma_32x32x32_i8(a, qreg[st], acc1);
+                    } else {
+                        acc0 = mfma_32x32x32_i8(a, qreg[st], acc0);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (DO_S) {
+                // dequantise here: the MFMA phase is the shorter one of the two
+                const float* ksl = sks[i & 1];
+#pragma unroll
+                for (int r4 = 0; r4 < 4; r4++) {
+                    const f4 ks0 = *reinterpret_cast<const f4*>(&ksl[8 * r4 + 4 * g]);
+                    const f4 ks1 = *reinterpret_cast<const f4*>(&ksl[32 + 8 * r4 + 4 * g]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        tsc[0][4 * r4 + e] = (float)acc0[4 * r4 + e] * ks0[e];
+                        tsc[1][4 * r4 + e] = (float)acc1[4 * r4 + e] * ks1[e];
+                    }
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (DO_S) {
-            // dequantise here: the MFMA phase is the shorter one of the two
-            const float* ksl = sks[i & 1];
+        };
+        auto phase_m = [&](int i) {
+            if (!wave_active) {
+                return;
+            }
+            const bool do_pv = i >= 1 && cls_prev != 0;
+            int cls_now = 0;
+            if (i < n) {
+                const int kt0 = (t_begin + i) * kI8BN;
+                cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kI8BN - 1);
+            }
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (do_pv && cls_now != 0) {
+                mfma_stream(T_{}, T_{}, i);
+            } else if (do_pv) {
+                mfma_stream(T_{}, F_{}, i);
+            } else if (cls_now != 0) {
+                mfma_stream(F_{}, T_{}, i);
+            }
+            cls_prev = cls_now;
+        };
+
+        // V(i): exact running max over the 64-key block, P as integers 0..127;
+        // O and l are rescaled whenever the max grows
+        auto phase_v = [&](int i) {
+            if (!wave_active || cls_prev == 0) {
+                return;
+            }
+            f16x t[2] = {tsc[0], tsc[1]};
+            if (!qpos) {
 #pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const f4 ks0 = *reinterpret_cast<const f4*>(&ksl[8 * r4 + 4 * g]);
-                const f4 ks1 = *reinterpret_cast<const f4*>(&ksl[32 + 8 * r4 + 4 * g]);
+                for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    tsc[0][4 * r4 + e] = (float)acc0[4 * r4 + e] * ks0[e];
-                    tsc[1][4 * r4 + e] = (float)acc1[4 * r4 + e] * ks1[e];
+                    for (int e = 0; e < 16; e++) {
+                        t[kt][e] *= qc;
+                    }
                 }
             }
+            if (cls_prev == 2) {
+                const int kt0 = (t_begin + i) * kI8BN;
+                const int a = row_lo - kt0 - 4 * g;
+                const int bnd = row_hi - kt0 - 4 * g;
+#pragma unroll
+                for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
+                        t[kt][e] = (off < a || off > bnd) ? -INFINITY : t[kt][e];
+                    }
+                }
+            }
+            float mx = t[0][0];
+#pragma unroll
+            for (int e = 1; e < 16; e++) {
+                mx = fmaxf(mx, t[0][e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                mx = fmaxf(mx, t[1][e]);
+            }
+            mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
+            const float m_new = fmaxf(m_run, mx);
+            const bool grow = m_new > m_run;
+            if (wave_any(grow)) {
+                const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
+                m_run = m_new;
+                l_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < C::NDT; dt++) {
+                    oacc[dt] *= alpha;
+                }
+            }
+            const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
+            float psum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const float y = fast_exp2(fmaf(t[kt][e], qeff, c0)); // 127 p, at most 127 (+ rounding)
+                    psum += y;
+                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
+                }
+            }
+            l_run += psum;
+        };
+
+        if (n > 0) {
+            load_pair(0);
+            store_pair(0);
+            load_pair(1);
         }
-    };
-    auto phase_m = [&](int i) {
+        __syncthreads();
+        if (n > 0) {
+            if (grp == 0) {
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 1);
+                    load_pair(i + 2);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+                __syncthreads();
+            } else {
+                store_pair(1);
+                load_pair(2);
+                __syncthreads();
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 2);
+                    load_pair(i + 3);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+            }
+        }
+
         if (!wave_active) {
             return;
         }
-        const bool do_pv = i >= 1 && cls_prev != 0;
-        int cls_now = 0;
-        if (i < n) {
-            const int kt0 = (t_begin + i) * kI8BN;
-            cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kI8BN - 1);
-        }
-        using T_ = std::true_type;
-        using F_ = std::false_type;
-        if (do_pv && cls_now != 0) {
-            mfma_stream(T_{}, T_{}, i);
-        } else if (do_pv) {
-            mfma_stream(T_{}, F_{}, i);
-        } else if (cls_now != 0) {
-            mfma_stream(F_{}, T_{}, i);
-        }
-        cls_prev = cls_now;
-    };
-
-    // V(i): exact running max over the 64-key block, P as integers 0..127;
-    // O and l are rescaled whenever the max grows
-    auto phase_v = [&](int i) {
-        if (!wave_active || cls_prev == 0) {
-            return;
-        }
-        f16x t[2] = {tsc[0], tsc[1]};
-        if (!qpos) {
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    t[kt][e] *= qc;
-                }
-            }
-        }
-        if (cls_prev == 2) {
-            const int kt0 = (t_begin + i) * kI8BN;
-            const int a = row_lo - kt0 - 4 * g;
-            const int bnd = row_hi - kt0 - 4 * g;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
-                    t[kt][e] = (off < a || off > bnd) ? -INFINITY : t[kt][e];
-                }
-            }
-        }
-        float mx = t[0][0];
-#pragma unroll
-        for (int e = 1; e < 16; e++) {
-            mx = fmaxf(mx, t[0][e]);
-        }
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            mx = fmaxf(mx, t[1][e]);
-        }
-        mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
-        const float m_new = fmaxf(m_run, mx);
-        const bool grow = m_new > m_run;
-        if (wave_any(grow)) {
-            const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
-            m_run = m_new;
-            l_run *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-                oacc[dt] *= alpha;
-            }
-        }
-        const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
-        float psum = 0.0f;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float y = fast_exp2(fmaf(t[kt][e], qeff, c0)); // 127 p, at most 127 (+ rounding)
-                psum += y;
-                pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
-            }
-        }
-        l_run += psum;
-    };
-
-    if (n > 0) {
-        load_pair(0);
-        store_pair(0);
-        load_pair(1);
-    }
-    __syncthreads();
-    if (n > 0) {
-        if (grp == 0) {
-            for (int i = 0; i < n; i++) {
-                phase_m(i);
-                __syncthreads();
-                store_pair(i + 1);
-                load_pair(i + 2);
-                phase_v(i);
-                __syncthreads();
-            }
-            phase_m(n);
-            __syncthreads();
-            __syncthreads();
-        } else {
-            store_pair(1);
-            load_pair(2);
-            __syncthreads();
-            for (int i = 0; i < n; i++) {
-                phase_m(i);
-                __syncthreads();
-                store_pair(i + 2);
-                load_pair(i + 3);
-                phase_v(i);
-                __syncthreads();
-            }
-            phase_m(n);
-            __syncthreads();
-        }
-    }
-
-    if (!wave_active) {
-        return;
-    }
-    const float l = pair_sum(l_run);
-    const float f = l > 0.0f ? p.v_scale / l : 0.0f;
-    if (q < p.Sq) {
-        _Float16* orow = obase + (int64_t)q * p.o_ss;
+        // O = O^T * v_scale / l (times the channel scales) through this wave's sO
+        // slot: written in the accumulator layout (lane = row), read back along
+        // rows and stored 16 bytes per lane, so every store instruction writes
+        // whole rows, non-temporal (O is not read again; streaming it past the L2
+        // keeps the K/V tiles the other row tiles reuse resident).
+        const float l = pair_sum(l_run);
+        const float f = l > 0.0f ? p.v_scale / l : 0.0f;
         // per-channel V scale of this kv head (1 when absent)
         const float* vch = p.vch != nullptr ? p.vch + ((int64_t)b * p.Hkv + kvh) * D : nullptr;
+        _Float16* const slot = sO + wave * 32 * C::LDO;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; dt++) {
 #pragma unroll
@@ -467,9 +479,37 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 }
                 h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * c[0]), (_Float16)(oacc[dt][4 * qq + 1] * c[1]),
                          (_Float16)(oacc[dt][4 * qq + 2] * c[2]), (_Float16)(oacc[dt][4 * qq + 3] * c[3])};
-                *reinterpret_cast<h4*>(orow + d0) = o4;
+                *reinterpret_cast<h4*>(slot + l32 * C::LDO + d0) = o4;
             }
         }
+        // LPR lanes per row, RPI rows per instruction; the indices come from an
+        // opaque copy of the lane id so that the compiler cannot hoist the
+        // addresses above the key-tile loop (they would stay live through it)
+        constexpr int OCH = D / 8; // 16-byte chunks per output row
+        constexpr int LPR = OCH <= 8 ? 8 : 16;
+        constexpr int RPI = 64 / LPR;
+        int lane_e = lane;
+        asm volatile("" : "+v"(lane_e));
+        const int r0 = lane_e / LPR;
+        const int ch = lane_e % LPR;
+        _Float16* const orow0 = obase + (int64_t)(q0 + r0) * p.o_ss + 8 * ch;
+#pragma unroll
+        for (int c = 0; c < 32 / RPI; c++) {
+            const int r = r0 + RPI * c;
+            if (ch < OCH) {
+                const h8 o8 = *reinterpret_cast<const h8*>(slot + r * C::LDO + 8 * ch);
+                if (q0 + r < p.Sq) {
+                    __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(orow0 + (int64_t)(RPI * c) * p.o_ss));
+                }
+            }
+        }
+    };
+    for (int item = 0;; item++) {
+        const int wg = persistent_item(blockIdx.x, gridDim.x, item, p.n_items);
+        if (wg < 0) {
+            break;
+        }
+        run_tile(wg);
     }
 }
 
@@ -508,8 +548,15 @@ __global__ __launch_bounds__(64) void int8_scores_kernel(const int8_t* __restric
 
 template <int D>
 int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    // persistent: as many workgroups as the device holds at once, each
+    // walking its share of the n_wg row tiles
+    const int64_t resident = resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D>), kI8Threads, err);
+    if (resident <= 0) {
+        return -1;
+    }
+    const int64_t grid = std::min(n_wg, resident);
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_int8<D>, dim3((uint32_t)n_wg), dim3(kI8Threads), 0, stream, p);
+    hipLaunchKernelGGL(fa_fwd_int8<D>, dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -565,6 +612,7 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
         err = "launch grid out of range";
         return -1;
     }
+    p.n_items = (int32_t)n_wg;
     switch (a.D) {
     case 64: return launch_int8<64>(p, n_wg, stream, err);
     case 128: return launch_int8<128>(p, n_wg, stream, err);

@@ -214,3 +214,42 @@ def test_int8_per_token_measured_workload_slice(gpu, oracle_lib):
     vscale = vch[:, :, None, :].repeat(hq // hkv, axis=1)
     mx, _, _ = errors(out.float().cpu().numpy() * vscale, emu * vscale)
     assert mx <= I8_MAX_ABS
+
+
+# Row tiles well beyond the resident grid (256 workgroups on 256 CUs), so every
+# persistent workgroup walks several tiles, with ragged ends.
+# name, b, hq, hkv, s, d, causal, window, v_channel
+PERSISTENT_CASES = [
+    ("d128_gqa4_causal", 2, 32, 8, 1100, 128, True, -1, False),  # 16 head groups x 18 row tiles
+    ("d64_mha_window", 4, 16, 16, 1500, 64, False, 300, False),  # 64 x 6
+    ("d128_gqa2_vchannel", 2, 16, 8, 1300, 128, False, -1, True),  # 16 x 11 + the fused channel scales
+]
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=[c[0] for c in PERSISTENT_CASES])
+def test_int8_persistent_workgroups_cover_every_tile(gpu, oracle_lib, case):
+    """Output pre-filled with NaN: a row tile that no workgroup writes fails
+    the finiteness check, one written wrongly fails the INT8 bar."""
+    import rdnattention_amd as ra
+
+    name, b, hq, hkv, s, d, causal, window, vchan = case
+    log(f"[int8 persistent] {name}")
+    g = torch.Generator().manual_seed(22)
+    qi, qsv = oracle.quant_pertoken(torch.randn(b, hq, s, d, generator=g).numpy())
+    ki, ksv = oracle.quant_pertoken(torch.randn(b, hkv, s, d, generator=g).numpy())
+    vf = torch.randn(b, hkv, s, d, generator=g).numpy()
+    vi, vch = oracle.quant_perchannel(vf)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    out = torch.full((b, hq, s, d), float("nan"), dtype=torch.float16, device=gpu)
+    ra.attention_int8_forward_into(t(qi), t(ki), t(vi), out, t(qsv), t(ksv), 1.0, is_causal=causal,
+                                   window_size=window, v_channel=t(vch) if vchan else None)
+    torch.cuda.synchronize()
+    emu = oracle.attention_int8(qi, ki, vi, qsv, ksv, 1.0, causal=causal, window=window)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    # compared at the channel scales (the kernel applies them itself when
+    # given v_channel); in int8 units (|o| up to 127) fp16 rounding alone
+    # would exceed the bar
+    vscale = np.repeat(vch, hq // hkv, axis=1)[:, :, None, :]
+    mx, _, _ = errors(got if vchan else got * vscale, emu * vscale)
+    assert mx <= I8_MAX_ABS, f"{name}: max_abs {mx:.3e}"
