@@ -198,6 +198,58 @@ __device__ __forceinline__ void wg_tile(int wg, int n_hg, int n_rt, int chunk, i
     }
 }
 
+// Output tile of one wave: 32 query rows (q0 + l32, l32 = lane % 32) x D
+// columns held as O^T MFMA accumulators (oacc[dt][4 qq + e] = column
+// dt*32 + 8 qq + 4 g + e, g = lane / 32), each scaled by factors(d0)[e] with
+// d0 = dt*32 + 8 qq + 4 g, rounded to fp16 and stored to rows q0 .. q0 + 31
+// (those < sq) at obase + row * o_ss. The tile passes through `slot`, 32 rows
+// at a stride of LDO halves in LDS that only this wave uses: written in the
+// accumulator layout, read back along rows and stored 16 bytes per lane, so
+// every store instruction writes whole rows (full cache lines). The stores
+// are non-temporal: the output is not read again, and streaming it past the
+// L2 keeps the K/V tiles that other row tiles reuse resident. (Stored from the
+// accumulator layout, one instruction writes 8 bytes of 32 rows, and such
+// partial lines must merge in the L2.)
+template <int D, int LDO, class Factors>
+__device__ __forceinline__ void store_o_tile(const f16x (&oacc)[D / 32], Factors&& factors, _Float16* slot,
+                                             _Float16* obase, int q0, int sq, int64_t o_ss, int lane) {
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) {
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int d0 = dt * 32 + 8 * qq + 4 * g;
+            const f4 c = factors(d0);
+            h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * c[0]), (_Float16)(oacc[dt][4 * qq + 1] * c[1]),
+                     (_Float16)(oacc[dt][4 * qq + 2] * c[2]), (_Float16)(oacc[dt][4 * qq + 3] * c[3])};
+            *reinterpret_cast<h4*>(slot + l32 * LDO + d0) = o4;
+        }
+    }
+    // LPR lanes per row (D/8 of them active), RPI rows per instruction; the
+    // indices come from an opaque copy of the lane id so that the compiler
+    // cannot hoist the addresses above the caller's key-tile loop (they would
+    // stay live through it)
+    constexpr int OCH = D / 8;
+    constexpr int LPR = OCH <= 4 ? 4 : (OCH <= 8 ? 8 : (OCH <= 16 ? 16 : 32));
+    constexpr int RPI = 64 / LPR;
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const int r0 = lane_e / LPR;
+    const int ch = lane_e % LPR;
+    _Float16* const orow0 = obase + (int64_t)(q0 + r0) * o_ss + 8 * ch;
+#pragma unroll
+    for (int c = 0; c < 32 / RPI; c++) {
+        const int r = r0 + RPI * c;
+        if (ch < OCH) {
+            const h8 o8 = *reinterpret_cast<const h8*>(slot + r * LDO + 8 * ch);
+            if (q0 + r < sq) {
+                __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(orow0 + (int64_t)(RPI * c) * o_ss));
+            }
+        }
+    }
+}
+
 // Work item `k` of persistent workgroup `w` in a grid of `P`, for `n` items
 // numbered like the workgroups of a one-item-per-workgroup grid (which
 // wg_tile places on XCD id % 8); -1 once the workgroup has none left.

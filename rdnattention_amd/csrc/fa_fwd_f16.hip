@@ -53,6 +53,7 @@ struct PrefillCfg {
     static constexpr int TASK = kBN * KCH;
     static constexpr int KT = (TASK + kThreads - 1) / kThreads;
     static constexpr int MIN_WG = D <= 128 ? 2 : 1;
+    static constexpr int LDO = D + 8; // output staging rows (halves)
 };
 
 // One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
@@ -293,21 +294,13 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     if (!wave_active) {
         return;
     }
-    // ---- normalise once in fp32, round once to fp16
+    // ---- normalise once in fp32, round once to fp16; the tile passes through
+    // this wave's part of the K/V buffers, free after the loop's last barrier
     const float l = pair_sum(l_run);
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (q < p.Sq) {
-        _Float16* orow = obase + (int64_t)q * p.o_ss;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
-                         (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
-                *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
-            }
-        }
-    }
+    static_assert(kWaves * 32 * C::LDO <= 2 * C::BUF_ELEMS, "output staging must fit the K/V buffers");
+    store_o_tile<D, C::LDO>(oacc, [&](int) { return f4{inv, inv, inv, inv}; }, smem + wave * 32 * C::LDO, obase, q0,
+                            p.Sq, p.o_ss, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -714,47 +707,12 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             }
         }
 
-        // O = O^T / l through this wave's sQ slot (free since read_q): written
-        // in the accumulator layout (lane = row), read back along rows and
-        // stored 16 bytes per lane, so every store instruction writes whole
-        // rows (full cache lines). Those go out non-temporal: O is not read
-        // again, and streaming it past the L2 keeps the K/V tiles the other row
-        // tiles reuse resident. (In the accumulator layout a store instruction
-        // writes 8 bytes of 32 rows; such partial lines must merge in the L2.)
+        // O = O^T / l, through this wave's sQ slot (free since read_q)
         if (wave_active) {
             const float l = pair_sum(l_run);
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            _Float16* const slot = sQ + wave * 32 * C::LDQ;
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-#pragma unroll
-                for (int qq = 0; qq < 4; qq++) {
-                    h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
-                             (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
-                    *reinterpret_cast<h4*>(slot + l32 * C::LDQ + dt * 32 + 8 * qq + 4 * g) = o4;
-                }
-            }
-            // LPR lanes per row (KCH of them active), RPI rows per instruction;
-            // the indices come from an opaque copy of the lane id so that the
-            // compiler cannot hoist the addresses above the key-tile loop
-            // (they would stay live through it)
-            constexpr int LPR = C::KCH <= 4 ? 4 : (C::KCH <= 8 ? 8 : 16);
-            constexpr int RPI = 64 / LPR;
-            int lane_e = lane;
-            asm volatile("" : "+v"(lane_e));
-            const int r0 = lane_e / LPR;
-            const int ch = lane_e % LPR;
-            _Float16* const orow0 = obase + (int64_t)(q0 + r0) * p.o_ss + 8 * ch;
-#pragma unroll
-            for (int c = 0; c < 32 / RPI; c++) {
-                const int r = r0 + RPI * c;
-                if (ch < C::KCH) {
-                    const h8 o8 = *reinterpret_cast<const h8*>(slot + r * C::LDQ + 8 * ch);
-                    if (q0 + r < p.Sq) {
-                        __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(orow0 + (int64_t)(RPI * c) * p.o_ss));
-                    }
-                }
-            }
+            store_o_tile<D, C::LDQ>(oacc, [&](int) { return f4{inv, inv, inv, inv}; }, sQ + wave * 32 * C::LDQ,
+                                    obase, q0, p.Sq, p.o_ss, lane);
         }
         if constexpr (C::PERSIST) {
             __syncthreads(); // the next row tile's Q staging writes every wave's slot

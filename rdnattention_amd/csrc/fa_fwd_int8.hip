@@ -453,56 +453,17 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         if (!wave_active) {
             return;
         }
-        // O = O^T * v_scale / l (times the channel scales) through this wave's sO
-        // slot: written in the accumulator layout (lane = row), read back along
-        // rows and stored 16 bytes per lane, so every store instruction writes
-        // whole rows, non-temporal (O is not read again; streaming it past the L2
-        // keeps the K/V tiles the other row tiles reuse resident).
+        // O = O^T * v_scale / l (times the per-channel V scales of this kv head
+        // when given), through this wave's sO slot
         const float l = pair_sum(l_run);
         const float f = l > 0.0f ? p.v_scale / l : 0.0f;
-        // per-channel V scale of this kv head (1 when absent)
         const float* vch = p.vch != nullptr ? p.vch + ((int64_t)b * p.Hkv + kvh) * D : nullptr;
-        _Float16* const slot = sO + wave * 32 * C::LDO;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                const int d0 = dt * 32 + 8 * qq + 4 * g;
-                float c[4] = {f, f, f, f};
-                if (vch != nullptr) {
-                    typedef float f4 __attribute__((ext_vector_type(4)));
-                    const f4 w = *reinterpret_cast<const f4*>(vch + d0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        c[e] = f * w[e];
-                    }
-                }
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * c[0]), (_Float16)(oacc[dt][4 * qq + 1] * c[1]),
-                         (_Float16)(oacc[dt][4 * qq + 2] * c[2]), (_Float16)(oacc[dt][4 * qq + 3] * c[3])};
-                *reinterpret_cast<h4*>(slot + l32 * C::LDO + d0) = o4;
-            }
-        }
-        // LPR lanes per row, RPI rows per instruction; the indices come from an
-        // opaque copy of the lane id so that the compiler cannot hoist the
-        // addresses above the key-tile loop (they would stay live through it)
-        constexpr int OCH = D / 8; // 16-byte chunks per output row
-        constexpr int LPR = OCH <= 8 ? 8 : 16;
-        constexpr int RPI = 64 / LPR;
-        int lane_e = lane;
-        asm volatile("" : "+v"(lane_e));
-        const int r0 = lane_e / LPR;
-        const int ch = lane_e % LPR;
-        _Float16* const orow0 = obase + (int64_t)(q0 + r0) * p.o_ss + 8 * ch;
-#pragma unroll
-        for (int c = 0; c < 32 / RPI; c++) {
-            const int r = r0 + RPI * c;
-            if (ch < OCH) {
-                const h8 o8 = *reinterpret_cast<const h8*>(slot + r * C::LDO + 8 * ch);
-                if (q0 + r < p.Sq) {
-                    __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(orow0 + (int64_t)(RPI * c) * p.o_ss));
-                }
-            }
-        }
+        store_o_tile<D, C::LDO>(
+            oacc,
+            [&](int d0) {
+                return vch != nullptr ? f * *reinterpret_cast<const f4*>(vch + d0) : f4{f, f, f, f};
+            },
+            sO + wave * 32 * C::LDO, obase, q0, p.Sq, p.o_ss, lane);
     };
     for (int item = 0;; item++) {
         const int wg = persistent_item(blockIdx.x, gridDim.x, item, p.n_items);
