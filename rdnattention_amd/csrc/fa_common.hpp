@@ -231,7 +231,8 @@ __device__ __forceinline__ void store_o_tile(const f16x (&oacc)[D / 32], Factors
     // cannot hoist the addresses above the caller's key-tile loop (they would
     // stay live through it)
     constexpr int OCH = D / 8;
-    constexpr int LPR = OCH <= 4 ? 4 : (OCH <= 8 ? 8 : (OCH <= 16 ? 16 : 32));
+    static_assert(D % 32 == 0 && OCH <= 64, "output tile width");
+    constexpr int LPR = OCH <= 4 ? 4 : (OCH <= 8 ? 8 : (OCH <= 16 ? 16 : (OCH <= 32 ? 32 : 64)));
     constexpr int RPI = 64 / LPR;
     int lane_e = lane;
     asm volatile("" : "+v"(lane_e));
