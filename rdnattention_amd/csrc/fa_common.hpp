@@ -307,6 +307,15 @@ __device__ __forceinline__ void dma_load16(i32x4_t rsrc, uint32_t voff, uint32_t
                  : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
                  : "memory", "m0");
 }
+// dma_load16 with the non-temporal cache policy, for bytes read exactly once
+// (split-K decode streams K/V once): they then do not displace lines that are
+// reused. Kernels whose workgroups share K/V through the L2 use dma_load16.
+__device__ __forceinline__ void dma_load16_nt(i32x4_t rsrc, uint32_t voff, uint32_t lds_byte_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
+                 : "memory", "m0");
+}
 
 // Bytes of a strided row range [row0, n_rows) of a row-major tensor with
 // `row_bytes` per row and `stride_bytes` between rows, clamped to 32 bits.

@@ -10,9 +10,10 @@
 //     one kv head and all M = (Hq/Hkv) * Sq query rows of that head group,
 //     packed as the 32 columns of one MFMA block (M <= 32)
 //   * its 4 waves work independently on interleaved 32-key tiles: each wave
-//     streams K and V with buffer_load ... lds (HBM -> LDS, no VGPR staging)
-//     into its own double-buffered LDS slice, two tiles in flight, no
-//     workgroup barriers in the loop
+//     streams K and V with buffer_load ... lds (HBM -> LDS, no VGPR staging),
+//     non-temporal since every byte is read once, into its own
+//     double-buffered LDS slice, two tiles in flight, no workgroup barriers in
+//     the loop
 //   * LDS rows are stored with an XOR swizzle of their 16-byte chunks so the
 //     ds_read_b128 of K (16 rows) and the ds_read_b64_tr_b16 of V (4 rows x
 //     32 B) both hit distinct banks although the DMA writes rows unpadded
@@ -156,11 +157,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa_fwd_f16_decode(DecodeParams
         const uint32_t sv = sk + C::TILE_BYTES;
 #pragma unroll
         for (int j = 0; j < C::DMA_PER_TILE; j++) {
-            dma_load16(rk, kdo[j], sk + 1024 * j);
+            dma_load16_nt(rk, kdo[j], sk + 1024 * j);
         }
 #pragma unroll
         for (int j = 0; j < C::DMA_PER_TILE; j++) {
-            dma_load16(rv, vdo[j], sv + 1024 * j);
+            dma_load16_nt(rv, vdo[j], sv + 1024 * j);
         }
     };
 
@@ -389,6 +390,11 @@ int launch_decode(const DecodeParams& p, int n_bkv, hipStream_t stream, std::str
     return 0;
 }
 
+template <int D>
+int64_t decode_resident(std::string& err) {
+    return resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_f16_decode<D>), kDecThreads, err);
+}
+
 } // namespace
 
 bool splitk_supported(const AttnArgs& a) {
@@ -425,14 +431,20 @@ int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::stri
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};
     p.rope_q = rope_q ? 1 : 0;
 
-    // splits: about two workgroups per CU (one resident at a time: the LDS
-    // ring is 128 KB), each split a whole number of 4-wave tile rounds.
-    // Measured on the B=16 Hkv=8 Sk=32768 cache: 512 workgroups stream
-    // 1-3 % faster than 1024 (fewer workgroup start-ups, smaller combine)
+    // splits: one round of workgroups over the device (as many as it holds at
+    // once: one per CU at D = 128, where the LDS ring is 128 KB), each split a
+    // whole number of 4-wave tile rounds. Measured on the B=16 Hkv=8
+    // Sk=32768 cache: 256 workgroups stream 1-4 % faster than 512 and
+    // 4-14 % faster than 1024 or 2048; uneven counts (384, 768) are slower.
     const int n_bkv = a.B * a.Hkv;
     const int round = kDecWaves * kDecTile;
     const int max_splits = std::max(1, (a.Sk + round - 1) / round);
-    int splits = std::max(1, std::min(max_splits, (512 + n_bkv - 1) / n_bkv));
+    const int64_t resident = a.D == 32 ? decode_resident<32>(err)
+                                       : (a.D == 64 ? decode_resident<64>(err) : decode_resident<128>(err));
+    if (resident <= 0) {
+        return -1;
+    }
+    int splits = (int)std::max<int64_t>(1, std::min<int64_t>(max_splits, (resident + n_bkv - 1) / n_bkv));
     int kps = (a.Sk + splits - 1) / splits;
     kps = std::max(round, (kps + round - 1) / round * round);
     splits = std::max(1, (a.Sk + kps - 1) / kps);
