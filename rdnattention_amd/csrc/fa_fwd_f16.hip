@@ -1,21 +1,24 @@
-// FP16 FlashAttention-2 forward for gfx950 (MI355X): prefill kernel and the
-// FP16 dispatcher.
+// FP16 FlashAttention-2 forward for gfx950 (MI355X): the prefill kernels for
+// head_dim <= 256 and the FP16 dispatcher.
 //
 // Replaces the reference's forwardKernel / forwardKernelGqa
-// (src/rdna/fa2_forward_f16.hip:633-877) with a CDNA4 MFMA design:
+// (src/rdna/fa2_forward_f16.hip:633-877) with CDNA4 MFMA designs:
 //
-//   * one workgroup = 4 waves; every wave owns 32 query rows of one head;
-//     a workgroup holds G query heads of one kv head (G | Hq/Hkv, G <= 4) so
-//     each K/V tile staged in LDS serves 128 (query, head) rows
+//   * fa_fwd_f16_pp<D> (D <= 128): 8 waves in two groups that alternate an
+//     MFMA phase and a softmax + staging phase (ping-pong, described above
+//     the kernel); persistent grid from D = 64 up; Q staged through LDS with
+//     row-contiguous loads; output stored through LDS as whole rows,
+//     non-temporal
+//   * fa_fwd_f16_prefill<D> (D 160..256): 4 waves, double-buffered K/V tiles,
+//     one barrier per tile
+//   * in both, every wave owns 32 query rows of one head and a workgroup holds
+//     G query heads of one kv head (G | Hq/Hkv, G <= 4), so each K/V tile
+//     staged in LDS serves all of them
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_f16: a lane owns one query column,
 //     so the row max/sum are lane-local plus one exchange across half-waves
 //   * P^T leaves the S^T accumulator in exactly the B-operand layout of the
-//     O^T = V^T P^T MFMA, so P never touches LDS
-//   * V is transposed into LDS (sVT[d][key]) with the key quads of every
-//     16-key group stored in the order 0,2,1,3 -- the order P^T's rows come
-//     out of the accumulator -- so each A operand is one 16-byte LDS read
-//   * LDS is double-buffered: tile t+1 is written while tile t is read, one
-//     barrier per tile; tile t+2 is in flight from HBM meanwhile
+//     O^T = V^T P^T MFMA, so P never touches LDS; V^T operands come from
+//     row-major V tiles through ds_read_b64_tr_b16 transpose reads
 //   * key tiles outside the causal/window band are skipped, tiles inside it
 //     run a mask-free path, only boundary tiles evaluate the mask
 //   * the running max is only raised when it grows by more than 2^8 (the

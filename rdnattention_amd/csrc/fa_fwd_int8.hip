@@ -26,7 +26,9 @@
 // two groups alternating MFMA and VALU phases, S^T = K Q^T so a lane owns one
 // query column, and P^T going from the S accumulator straight into the B
 // operand of O^T = V^T P^T.  V is converted to fp16 while it is staged into
-// LDS and its V^T operands come from ds_read_b64_tr_b16 transpose reads.
+// LDS and its V^T operands come from ds_read_b64_tr_b16 transpose reads.  The
+// grid is persistent (persistent_item), and O leaves through an LDS buffer as
+// whole-row non-temporal stores (store_o_tile).
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
