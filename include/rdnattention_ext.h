@@ -72,13 +72,21 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
  * 16-byte aligned, strides multiples of 16 bytes; head_dim a multiple of 8
  * up to 512.  q_out: int8 [batch, num_heads, seq_len, head_dim] contiguous;
  * scale_out: fp32, [batch, num_heads, seq_len] or [batch, num_heads,
- * head_dim], contiguous.  Returns 0, or -3 with "Quantize (int8) failed: ...".
+ * head_dim], contiguous.
+ * rot_cos / rot_sin (per token only; both or neither, nullptr = none): fp32
+ * RoPE tables [>= seq_len, head_dim / 2], contiguous, 16-byte aligned, as
+ * for rdna_attention_forward.  Each row (position s) is rotated first, with
+ * the FP16 attention path's arithmetic (pairs rotated in fp32, rounded to
+ * fp16 for fp16 input), and the rotated row is quantised: INT8 attention
+ * with RoPE, which the reference does not offer.
+ * Returns 0, or -3 with "Quantize (int8) failed: ...".
  * No reference counterpart (the reference quantises with torch ops). */
 RDNA_API int32_t rdna_quantize_int8(
     const void* x, int32_t x_dtype,
     int64_t x_stride_b, int64_t x_stride_h, int64_t x_stride_s,
     uint32_t batch_size, uint32_t num_heads, uint32_t seq_len, uint32_t head_dim,
-    int32_t per_channel, void* q_out, void* scale_out, void* hip_stream);
+    int32_t per_channel, const void* rot_cos, const void* rot_sin,
+    void* q_out, void* scale_out, void* hip_stream);
 
 /* Kernel timer.  While enabled, each launch of a main attention kernel
  * (prefill, split-K, int8; not the RoPE pre-rotation or split-K combine

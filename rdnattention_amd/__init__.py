@@ -88,7 +88,7 @@ def _lib_handle():
         lib.rdna_attention_forward_int8qk.restype = _I32
         lib.rdna_attention_forward_int8qk_vchannel.argtypes = _I8_ARGS[:-3] + [_VP] + _I8_ARGS[-3:]
         lib.rdna_attention_forward_int8qk_vchannel.restype = _I32
-        lib.rdna_quantize_int8.argtypes = [_VP, _I32] + [_I64] * 3 + [_U32] * 4 + [_I32, _VP, _VP, _VP]
+        lib.rdna_quantize_int8.argtypes = [_VP, _I32] + [_I64] * 3 + [_U32] * 4 + [_I32, _VP, _VP, _VP, _VP, _VP]
         lib.rdna_quantize_int8.restype = _I32
         lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
         lib.rdna_int8_qk_scores.restype = _I32
@@ -381,10 +381,12 @@ class KernelTimer:
         return False
 
 
-def _quantize_gpu(x, per_channel: bool):
+def _quantize_gpu(x, per_channel: bool, rot_cos=None, rot_sin=None):
     """rdna_quantize_int8 on a HIP tensor [B, H, S, D]: (int8 [B, H, S, D]
     contiguous, float32 scales [B, H, S] per token or [B, H, D] per channel),
-    bit-identical to the torch formulas of the reference wrapper."""
+    bit-identical to the torch formulas of the reference wrapper.  With
+    rot_cos/rot_sin (per token only) the rows are RoPE-rotated first, with the
+    FP16 attention path's arithmetic."""
     import torch
 
     if x.dim() != 4:
@@ -398,13 +400,16 @@ def _quantize_gpu(x, per_channel: bool):
     b, h, s, d = x.shape
     if d % 8 != 0 or d > 512:
         raise RDNAttentionError(f"GPU quantiser: head_dim {d} must be a multiple of 8 up to 512")
+    cos_ptr, sin_ptr, has_rope = _rope_ptrs(rot_cos, rot_sin, x, s, s, d)
+    if has_rope and per_channel:
+        raise ValueError("RoPE applies to the per-token (query/key) quantiser only")
     q = torch.empty((b, h, s, d), dtype=torch.int8, device=x.device)
     sc = torch.ones((b, h, d) if per_channel else (b, h, s), dtype=torch.float32, device=x.device)
     if q.numel() == 0:
         return q, sc
     st = x.stride()
     rc = _lib_handle().rdna_quantize_int8(x.data_ptr(), dt, st[0], st[1], st[2], b, h, s, d, 1 if per_channel else 0,
-                                          q.data_ptr(), sc.data_ptr(), _stream())
+                                          cos_ptr, sin_ptr, q.data_ptr(), sc.data_ptr(), _stream())
     if rc != 0:
         raise RDNAttentionError(f"quantisation failed: {last_error()}")
     return q, sc
@@ -438,17 +443,43 @@ def quantize_int8_perchannel_v(query, key, value):
     return qi, ki, vi, q_scale, k_scale, 1.0, v_channel.squeeze(-2)
 
 
-def quantize_int8_qk_pertoken(query, key):
+def _rope_torch(x, rot_cos, rot_sin):
+    """RoPE of a [B, H, S, D] tensor in torch (interleaved pairs, position =
+    row index, fp32 arithmetic, the result in x's dtype when that is fp16),
+    for CPU tensors; the GPU quantiser fuses the same rotation."""
+    import torch
+
+    xf = x.float()
+    n = x.shape[-2]
+    c = rot_cos[:n].to(xf.device)
+    sn = rot_sin[:n].to(xf.device)
+    a, b = xf[..., 0::2], xf[..., 1::2]
+    y = torch.empty_like(xf)
+    y[..., 0::2] = a * c - b * sn
+    y[..., 1::2] = a * sn + b * c
+    return y.to(torch.float16) if x.dtype == torch.float16 else y
+
+
+def quantize_int8_qk_pertoken(query, key, rot_cos=None, rot_sin=None):
     """(qi, ki, q_scale, k_scale) with one fp32 scale per (batch, head, row)
     (rdnattention/__init__.py:327-343).  HIP tensors are quantised by a
     library kernel (rdna_quantize_int8), bit-identical to the torch formulas
-    used for CPU tensors."""
+    used for CPU tensors.
+
+    rot_cos/rot_sin (an extension; the reference has no INT8 RoPE): fp32
+    [positions, head_dim // 2] tables as for flash_attn.  Query and key rows
+    are RoPE-rotated, as the FP16 path rotates them, before quantisation."""
     import torch
 
     if query.is_cuda and key.is_cuda:
-        qi, q_scale = _quantize_gpu(query, per_channel=False)
-        ki, k_scale = _quantize_gpu(key, per_channel=False)
+        qi, q_scale = _quantize_gpu(query, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
+        ki, k_scale = _quantize_gpu(key, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
         return qi, ki, q_scale, k_scale
+    if (rot_cos is None) != (rot_sin is None):
+        raise ValueError("pass both rot_cos and rot_sin, or neither")
+    if rot_cos is not None:
+        query = _rope_torch(query, rot_cos, rot_sin)
+        key = _rope_torch(key, rot_cos, rot_sin)
 
     def per_token(x):
         x = x.float()
@@ -461,9 +492,15 @@ def quantize_int8_qk_pertoken(query, key):
     return qi, ki, q_scale, k_scale
 
 
-def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, window_size: int = -1):
+def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, window_size: int = -1, rot_cos=None,
+                                rot_sin=None):
     """INT8 attention from ordinary fp16/fp32 Q/K/V (rdnattention/__init__.py:346-357):
     per-token Q/K scales and a per-channel V scale.
+
+    rot_cos/rot_sin (an extension; the reference has no INT8 RoPE): fp32
+    [positions, head_dim // 2] tables as for flash_attn.  Q and K are rotated
+    inside the per-token quantiser (the FP16 path's arithmetic), so RoPE costs
+    no extra pass.
 
     Three quantiser kernels and one attention kernel: the per-channel V
     rescale is applied in the attention kernel's epilogue
@@ -493,8 +530,9 @@ def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, wind
     _check_head_dim(query.shape[-1], "flash_attn_int8qk", allowed=SUPPORTED_HEAD_DIMS_INT8)
     if not has_device():
         raise RDNAttentionError("no usable HIP device found")
-    qi, q_scale = _quantize_gpu(query, per_channel=False)
-    ki, k_scale = _quantize_gpu(key, per_channel=False)
+    _rope_ptrs(rot_cos, rot_sin, query, query.shape[2], key.shape[2], query.shape[3])
+    qi, q_scale = _quantize_gpu(query, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
+    ki, k_scale = _quantize_gpu(key, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
     vi, v_channel = _quantize_gpu(value, per_channel=True)
     output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
     if output.numel() == 0:

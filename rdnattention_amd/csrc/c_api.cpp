@@ -298,8 +298,8 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
 
 RDNA_API int32_t rdna_quantize_int8(const void* x, int32_t x_dtype, int64_t x_stride_b, int64_t x_stride_h,
                                     int64_t x_stride_s, uint32_t batch_size, uint32_t num_heads, uint32_t seq_len,
-                                    uint32_t head_dim, int32_t per_channel, void* q_out, void* scale_out,
-                                    void* hip_stream) {
+                                    uint32_t head_dim, int32_t per_channel, const void* rot_cos,
+                                    const void* rot_sin, void* q_out, void* scale_out, void* hip_stream) {
     std::string err;
     const int64_t mult = x_dtype == 1 ? 4 : 8; // elements per 16 bytes
     if (x_dtype != 0 && x_dtype != 1) {
@@ -316,6 +316,12 @@ RDNA_API int32_t rdna_quantize_int8(const void* x, int32_t x_dtype, int64_t x_st
         err = "x and q_out must be 16-byte aligned, scale_out 4-byte aligned";
     } else if (x_stride_b % mult != 0 || x_stride_h % mult != 0 || x_stride_s % mult != 0) {
         err = "batch/head/seq strides of x must be multiples of 16 bytes";
+    } else if ((rot_cos == nullptr) != (rot_sin == nullptr)) {
+        err = "pass both rot_cos and rot_sin, or neither";
+    } else if (rot_cos != nullptr && per_channel != 0) {
+        err = "RoPE applies to the per-token scheme only";
+    } else if (!aligned(rot_cos, 16) || !aligned(rot_sin, 16)) {
+        err = "rot_cos and rot_sin must be 16-byte aligned";
     } else {
         rdna_amd::QuantArgs a;
         a.x = x;
@@ -326,6 +332,8 @@ RDNA_API int32_t rdna_quantize_int8(const void* x, int32_t x_dtype, int64_t x_st
         a.S = (int32_t)seq_len;
         a.D = (int32_t)head_dim;
         a.per_channel = per_channel != 0 ? 1 : 0;
+        a.rot_cos = static_cast<const float*>(rot_cos);
+        a.rot_sin = static_cast<const float*>(rot_sin);
         a.q = q_out;
         a.scale = static_cast<float*>(scale_out);
         if (rdna_amd::quantize_int8(a, static_cast<hipStream_t>(hip_stream), err) == 0) {

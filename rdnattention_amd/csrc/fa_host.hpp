@@ -45,6 +45,8 @@ struct QuantArgs {
     int64_t xs[3] = {0, 0, 0};
     int32_t B = 0, H = 0, S = 0, D = 0;
     int32_t per_channel = 0;
+    const float* rot_cos = nullptr; // per token only: RoPE tables [>= S, D/2] fp32, or null
+    const float* rot_sin = nullptr;
     void* q = nullptr;
     float* scale = nullptr;
 };

@@ -15,6 +15,12 @@
 // round-half-to-even like torch.round.  (torch on the CPU divides amax by 127
 // instead, which can differ in the last bit of the scale.)
 //
+// The per-token scheme can rotate the rows first (RoPE with the attention
+// kernels' tables and arithmetic: interleaved pairs rotated in fp32 and, for
+// fp16 input, rounded to fp16 exactly as the FP16 path rotates Q and K), so
+// that INT8 attention with RoPE quantises the rotated Q and K in one pass.
+// The reference has no INT8 RoPE.
+//
 // These kernels are HBM-bound streaming passes (read x once, write q once; the
 // per-channel scheme reads x twice: column maxima, then quantisation).
 #include "fa_common.hpp"
@@ -67,13 +73,46 @@ __device__ __forceinline__ void store8(int8_t* p, const float (&v)[8], float s) 
     *reinterpret_cast<i8x8_t*>(p) = o;
 }
 
+// RoPE of the 8-element chunk `sub` of a row at position s (tables
+// [positions, D/2] fp32): the pairs rotated in fp32 (rope8_cs, the FP16
+// kernels' arithmetic), rounded to fp16 for fp16 input.
+template <typename T>
+__device__ __forceinline__ void rope_chunk(float (&v)[8], const float* cos_t, const float* sin_t, int s, int D,
+                                           int sub) {
+    const f4 c = *reinterpret_cast<const f4*>(cos_t + (int64_t)s * (D / 2) + 4 * sub);
+    const f4 sn = *reinterpret_cast<const f4*>(sin_t + (int64_t)s * (D / 2) + 4 * sub);
+    if constexpr (sizeof(T) == 2) {
+        h8 x;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            x[e] = (_Float16)v[e]; // exact: v holds fp16 values
+        }
+        const h8 y = rope8_cs(x, c, sn);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            v[e] = (float)y[e];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float a = v[2 * i];
+            const float b = v[2 * i + 1];
+            v[2 * i] = a * c[i] - b * sn[i];
+            v[2 * i + 1] = a * sn[i] + b * c[i];
+        }
+    }
+}
+
 // Per-token: LPR lanes (a power of two >= D/8) per row, each holding one
 // 8-element chunk; 256 / LPR rows per block iteration, grid-stride over rows.
+// With rot_cos (and rot_sin) the rows are rotated by RoPE before quantisation.
 template <typename T, int LPR>
 __global__ __launch_bounds__(kQThreads) void quant_rows_kernel(const T* __restrict__ x, int8_t* __restrict__ q,
-                                                               float* __restrict__ scale, int64_t sb, int64_t sh,
-                                                               int64_t ss, int32_t H, int32_t S, int32_t D,
-                                                               int64_t n_rows) {
+                                                               float* __restrict__ scale,
+                                                               const float* __restrict__ rot_cos,
+                                                               const float* __restrict__ rot_sin, int64_t sb,
+                                                               int64_t sh, int64_t ss, int32_t H, int32_t S,
+                                                               int32_t D, int64_t n_rows) {
     constexpr int RPB = kQThreads / LPR; // rows per block iteration
     const int tid = threadIdx.x;
     const int sub = tid % LPR;
@@ -89,6 +128,9 @@ __global__ __launch_bounds__(kQThreads) void quant_rows_kernel(const T* __restri
             const int64_t b = bh / H;
             const int h = (int)(bh - b * H);
             load8(x + b * sb + h * sh + (int64_t)s * ss + 8 * sub, v);
+            if (rot_cos != nullptr) {
+                rope_chunk<T>(v, rot_cos, rot_sin, s, D, sub);
+            }
         }
         float m = 0.0f;
 #pragma unroll
@@ -213,8 +255,8 @@ int launch_rows(const QuantArgs& a, hipStream_t stream) {
         constexpr int RPB = kQThreads / LPR;
         const int64_t blocks = std::min<int64_t>((n_rows + RPB - 1) / RPB, 65536);
         hipLaunchKernelGGL((quant_rows_kernel<T, LPR>), dim3((uint32_t)blocks), dim3(kQThreads), 0, stream,
-                           static_cast<const T*>(a.x), static_cast<int8_t*>(a.q), a.scale, a.xs[0], a.xs[1],
-                           a.xs[2], a.H, a.S, a.D, n_rows);
+                           static_cast<const T*>(a.x), static_cast<int8_t*>(a.q), a.scale, a.rot_cos, a.rot_sin,
+                           a.xs[0], a.xs[1], a.xs[2], a.H, a.S, a.D, n_rows);
     };
     if (ch <= 4) {
         go(std::integral_constant<int, 4>{});
@@ -254,6 +296,10 @@ int launch_cols(const QuantArgs& a, hipStream_t stream, std::string& err) {
 
 int quantize_int8(const QuantArgs& a, hipStream_t stream, std::string& err) {
     int rc;
+    if (a.per_channel && a.rot_cos != nullptr) {
+        err = "RoPE applies to the per-token scheme only";
+        return -1;
+    }
     if (a.per_channel) {
         rc = a.x_fp32 ? launch_cols<float>(a, stream, err) : launch_cols<_Float16>(a, stream, err);
     } else {

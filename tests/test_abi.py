@@ -203,11 +203,12 @@ def test_kernel_timer_without_launches(lib):
 
 def _quant(lib, **kw):
     hold, p = _buf()
-    args = dict(x=p, dtype=0, strides=(8 * 16 * 64, 16 * 64, 64), B=1, H=8, S=16, D=64, per_channel=0, q=p, sc=p)
+    args = dict(x=p, dtype=0, strides=(8 * 16 * 64, 16 * 64, 64), B=1, H=8, S=16, D=64, per_channel=0, cos=None,
+                sin=None, q=p, sc=p)
     args.update(kw)
     s = args["strides"]
     rc = lib.rdna_quantize_int8(args["x"], args["dtype"], *s, args["B"], args["H"], args["S"], args["D"],
-                                args["per_channel"], args["q"], args["sc"], None)
+                                args["per_channel"], args["cos"], args["sin"], args["q"], args["sc"], None)
     return rc, lib.rdna_get_error().decode()
 
 
@@ -219,8 +220,13 @@ def _quant(lib, **kw):
     (dict(x=None), "null tensor pointer"),
     (dict(strides=(8192, 1024, 68)), "strides of x must be multiples of 16 bytes"),
     (dict(dtype=1, strides=(8192, 1024, 66)), "strides of x must be multiples of 16 bytes"),
+    (dict(cos="p"), "pass both rot_cos and rot_sin, or neither"),
+    (dict(cos="p", sin="p", per_channel=1), "RoPE applies to the per-token scheme only"),
+    (dict(cos="p+4", sin="p"), "rot_cos and rot_sin must be 16-byte aligned"),
 ])
 def test_quantize_argument_errors(lib, kw, msg):
+    hold, p = _buf()
+    kw = {k: (p if v == "p" else p + 4 if v == "p+4" else v) for k, v in kw.items()}
     rc, err = _quant(lib, **kw)
     assert rc == -3
     assert err.startswith("Quantize (int8) failed: ")
@@ -234,3 +240,27 @@ def test_int8_vchannel_misaligned_rejected(lib):
                                                      1.0, None, None, p + 4, 0, -1, None)
     assert rc == -3
     assert "v_channel_vec must be a 16-byte aligned float array" in lib.rdna_get_error().decode()
+
+
+def test_pertoken_rope_cpu_path_matches_oracle():
+    """quantize_int8_qk_pertoken on CPU tensors with RoPE tables: the torch
+    rotation equals the oracle's (fp32 products, fp16 rounding) and the rows
+    are then quantised by the reference formulas."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import rdnattention_amd as ra
+
+    g = torch.Generator().manual_seed(17)
+    q = torch.randn(1, 2, 40, 64, generator=g).half()
+    k = torch.randn(1, 2, 40, 64, generator=g).half()
+    cos, sin = oracle.rope_tables(40, 64)
+    qi, ki, qs, ks = ra.quantize_int8_qk_pertoken(q, k, rot_cos=torch.from_numpy(cos), rot_sin=torch.from_numpy(sin))
+    for x, xi, xs in ((q, qi, qs), (k, ki, ks)):
+        rot = oracle.rope(x.float().numpy(), cos, sin, round_f16=True)
+        assert np.array_equal(ra._rope_torch(x, torch.from_numpy(cos), torch.from_numpy(sin)).float().numpy(), rot)
+        ri, rs = oracle.quant_pertoken(rot)
+        assert np.array_equal(xi.numpy(), ri) and np.allclose(xs.numpy(), rs, rtol=1e-6, atol=0)
+    with pytest.raises(ValueError, match="both"):
+        ra.quantize_int8_qk_pertoken(q, k, rot_cos=torch.from_numpy(cos))

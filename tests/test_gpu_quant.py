@@ -172,3 +172,77 @@ def test_quantized_end_to_end_matches_reference_composition(gpu, hkv):
     diff = (out.float() - ref.float()).abs()
     log(f"[quant]   vs composition max={diff.max().item():.2e}")
     assert torch.allclose(out.float(), ref.float(), rtol=2e-3, atol=2e-3)
+
+
+# INT8 with RoPE (an extension: the reference has no INT8 RoPE). The per-token
+# quantiser rotates each row with the FP16 path's arithmetic before scaling.
+# The oracle rotates in numpy (each product rounded); the kernel may contract a
+# product into an FMA, so a rotated value can differ in its last fp16 bit:
+# int8 values may then differ by one and scales by an fp16 ulp, rarely.
+ROPE_SHAPES = [(1, 4, 70, 64), (2, 3, 33, 128), (1, 2, 300, 256), (1, 2, 40, 512)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("shape", ROPE_SHAPES, ids=[f"{s[2]}x{s[3]}" for s in ROPE_SHAPES])
+def test_pertoken_rope_quantiser(gpu, dtype, shape):
+    import rdnattention_amd as ra
+
+    log(f"[quant] pertoken rope {shape} {dtype}")
+    b, h, s, d = shape
+    g = torch.Generator().manual_seed(15)
+    x = (torch.randn(b, h, s, d, generator=g) * 3.0).to(dtype)
+    cos, sin = oracle.rope_tables(s + 5, d)
+    qi, qs = ra._quantize_gpu(x.to(gpu), per_channel=False, rot_cos=torch.from_numpy(cos).to(gpu),
+                              rot_sin=torch.from_numpy(sin).to(gpu))
+    rot = torch.from_numpy(oracle.rope(x.float().numpy(), cos, sin, round_f16=dtype == torch.float16))
+    ti, ts = torch_pertoken(rot.to(dtype).to(gpu))
+    torch.cuda.synchronize()
+    assert torch.allclose(qs, ts, rtol=2e-3, atol=0)
+    di = (qi.int() - ti.int()).abs()
+    assert di.max().item() <= 1
+    assert (di > 0).float().mean().item() < 2e-3
+    # the same rows unrotated are quantised as without tables
+    ui, us = ra._quantize_gpu(x.to(gpu), per_channel=False)
+    pi, ps = torch_pertoken(x.to(gpu))
+    assert torch.equal(ui, pi) and torch.equal(us, ps)
+
+
+def test_rope_quantiser_rejects_per_channel(gpu):
+    import rdnattention_amd as ra
+
+    x = torch.randn(1, 2, 16, 64, device=gpu)
+    cos, sin = oracle.rope_tables(16, 64)
+    with pytest.raises(ValueError, match="per-token"):
+        ra._quantize_gpu(x, per_channel=True, rot_cos=torch.from_numpy(cos).to(gpu),
+                         rot_sin=torch.from_numpy(sin).to(gpu))
+
+
+@pytest.mark.parametrize("causal,hkv", [(True, 2), (False, 8)], ids=["causal_gqa4", "dense_mha"])
+def test_quantized_rope_end_to_end(gpu, oracle_lib, causal, hkv):
+    """flash_attn_int8qk_quantized with RoPE against the kernel-exact INT8
+    emulation of the oracle-rotated, oracle-quantised inputs (INT8 bar, at the
+    channel scales)."""
+    import rdnattention_amd as ra
+
+    log(f"[quant] rope end to end causal={causal} hkv={hkv}")
+    g = torch.Generator().manual_seed(16)
+    b, hq, s, d = 2, 8, 300, 128
+    q = torch.randn(b, hq, s, d, generator=g).half()
+    k = torch.randn(b, hkv, s, d, generator=g).half()
+    v = torch.randn(b, hkv, s, d, generator=g).half()
+    cos, sin = oracle.rope_tables(s, d)
+    out = ra.flash_attn_int8qk_quantized(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal,
+                                         rot_cos=torch.from_numpy(cos).to(gpu), rot_sin=torch.from_numpy(sin).to(gpu))
+    torch.cuda.synchronize()
+    qr = oracle.rope(q.float().numpy(), cos, sin, round_f16=True)
+    kr = oracle.rope(k.float().numpy(), cos, sin, round_f16=True)
+    qi, qsv = oracle.quant_pertoken(qr)
+    ki, ksv = oracle.quant_pertoken(kr)
+    vi, vc = oracle.quant_perchannel(v.float().numpy())
+    emu = oracle.attention_int8(qi, ki, vi, qsv, ksv, 1.0, causal=causal)
+    vscale = np.repeat(vc, hq // hkv, axis=1)[:, :, None, :]
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    mx, mean, _ = errors(got, emu * vscale)
+    log(f"[quant]   vs emulation max={mx:.2e} mean={mean:.2e}")
+    assert mx <= I8_MAX_ABS
