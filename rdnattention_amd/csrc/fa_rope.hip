@@ -92,11 +92,24 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
     if (bytes == 0) {
         return 0;
     }
-    hipMemPool_t pool = nullptr;
-    if (scratch_pool(pool, err) != 0) {
+    // Under graph capture the allocation becomes a memory node the graph
+    // owns: take it with hipMallocAsync (the device's default pool), which
+    // graph capture supports; otherwise from the retaining pool.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(s, &capture);
+    if (e != hipSuccess) {
+        err = std::string("scratch allocation failed: ") + hipGetErrorString(e);
         return -1;
     }
-    hipError_t e = hipMallocFromPoolAsync(&ptr, bytes, pool, s);
+    if (capture != hipStreamCaptureStatusNone) {
+        e = hipMallocAsync(&ptr, bytes, s);
+    } else {
+        hipMemPool_t pool = nullptr;
+        if (scratch_pool(pool, err) != 0) {
+            return -1;
+        }
+        e = hipMallocFromPoolAsync(&ptr, bytes, pool, s);
+    }
     if (e != hipSuccess) {
         ptr = nullptr;
         err = std::string("scratch allocation failed: ") + hipGetErrorString(e);
