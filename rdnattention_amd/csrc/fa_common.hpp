@@ -327,6 +327,19 @@ __device__ __forceinline__ uint32_t range_bytes(int64_t rows_left, int64_t strid
     return n > 0xffffffffll ? 0xffffffffu : (uint32_t)n;
 }
 
+// Bytes of one key tile: min(rows_left, TILE_ROWS) rows of row_bytes at a
+// stride of stride_bytes (<= 2^25 and TILE_ROWS <= 64, so the result fits 32
+// bits), 0 when rows_left <= 0.
+template <int TILE_ROWS>
+__device__ __forceinline__ uint32_t tile_bytes(int rows_left, uint32_t stride_bytes, uint32_t row_bytes) {
+    static_assert(TILE_ROWS <= 64, "tile byte range must fit 32 bits");
+    if (rows_left <= 0) {
+        return 0;
+    }
+    const uint32_t rows = (uint32_t)(rows_left < TILE_ROWS ? rows_left : TILE_ROWS);
+    return (rows - 1) * stride_bytes + row_bytes;
+}
+
 // RoPE on 8 consecutive channels (4 interleaved pairs) of one row:
 // (a, b) -> (a*c - b*s, a*s + b*c) in fp32, rounded to fp16, where c/s are
 // table columns col0 .. col0+3 (src/rdna/fa2_forward_f16.hip:63-77).

@@ -481,6 +481,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             n = khi / kBN + 1 - t_begin;
         }
         const int Sk = p.mask.sk;
+        const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
 
@@ -503,13 +504,16 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
 
         h8 kreg[C::CT], vreg[C::CT];
         // registers <- HBM for pair x (K tile x if x < n, V tile x-1 if 1 <= x <= n);
-        // a missing tile gets num_records 0, so its loads return 0 and touch nothing
+        // a missing tile gets num_records 0, so its loads return 0 and touch nothing.
+        // A tile spans at most kBN rows at a seq stride <= 2^24 elements, so its
+        // byte range fits 32 bits (tile_bytes); this keeps the per-tile
+        // descriptor set-up to a few scalar instructions.
         auto load_pair = [&](int x) {
             const int tk = t_begin + x, tv = t_begin + x - 1;
             const auto rk = make_rsrc(kbase + (int64_t)tk * kBN * p.k_ss,
-                                      x < n ? range_bytes(Sk - tk * kBN, p.k_ss * 2, D * 2) : 0u);
+                                      x < n ? tile_bytes<kBN>(Sk - tk * kBN, k_row_b, D * 2) : 0u);
             const auto rv = make_rsrc(vbase + (int64_t)tv * kBN * p.v_ss,
-                                      (x >= 1 && x <= n) ? range_bytes(Sk - tv * kBN, p.v_ss * 2, D * 2) : 0u);
+                                      (x >= 1 && x <= n) ? tile_bytes<kBN>(Sk - tv * kBN, v_row_b, D * 2) : 0u);
 #pragma unroll
             for (int it = 0; it < C::CT; it++) {
                 kreg[it] = buffer_load_h8(rk, coff_k[it], 0);

@@ -230,9 +230,9 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         auto load_pair = [&](int x) {
             const int tk = t_begin + x, tv = t_begin + x - 1;
             const auto rk = make_rsrc(kbase + (int64_t)tk * kI8BN * p.k_ss,
-                                      x < n ? range_bytes(Sk - tk * kI8BN, p.k_ss, D) : 0u);
+                                      x < n ? tile_bytes<kI8BN>(Sk - tk * kI8BN, (uint32_t)p.k_ss, D) : 0u);
             const auto rv = make_rsrc(vbase + (int64_t)tv * kI8BN * p.v_ss,
-                                      (x >= 1 && x <= n) ? range_bytes(Sk - tv * kI8BN, p.v_ss, D) : 0u);
+                                      (x >= 1 && x <= n) ? tile_bytes<kI8BN>(Sk - tv * kI8BN, (uint32_t)p.v_ss, D) : 0u);
 #pragma unroll
             for (int it = 0; it < C::CT; it++) {
                 kreg[it] = buffer_load_i4(rk, coff_k[it]);
