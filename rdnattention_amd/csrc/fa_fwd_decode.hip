@@ -151,8 +151,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa_fwd_f16_decode(DecodeParams
     }
     auto issue_tile = [&](int j_tile, int slot) {
         const int kt0 = (t0 + wave + kDecWaves * j_tile) * kDecTile;
-        const i32x4_t rk = make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, range_bytes(p.mask.sk - kt0, p.k_ss * 2, D * 2));
-        const i32x4_t rv = make_rsrc_v(vbase + (int64_t)kt0 * p.v_ss, range_bytes(p.mask.sk - kt0, p.v_ss * 2, D * 2));
+        const i32x4_t rk = make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kDecTile>(p.mask.sk - kt0, (uint32_t)(p.k_ss * 2), D * 2));
+        const i32x4_t rv = make_rsrc_v(vbase + (int64_t)kt0 * p.v_ss, tile_bytes<kDecTile>(p.mask.sk - kt0, (uint32_t)(p.v_ss * 2), D * 2));
         const uint32_t sk = (uint32_t)reinterpret_cast<uintptr_t>(wsm + slot * C::SLOT_BYTES);
         const uint32_t sv = sk + C::TILE_BYTES;
 #pragma unroll

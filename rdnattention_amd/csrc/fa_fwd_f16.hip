@@ -238,8 +238,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     // tile; rows past Sk fall outside num_records and read as 0.
     auto load_kv = [&](int t) {
         const int kt0 = t * kBN;
-        const auto rk = make_rsrc(kbase + (int64_t)kt0 * p.k_ss, range_bytes(Sk - kt0, p.k_ss * 2, D * 2));
-        const auto rv = make_rsrc(vbase + (int64_t)kt0 * p.v_ss, range_bytes(Sk - kt0, p.v_ss * 2, D * 2));
+        const auto rk = make_rsrc(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kBN>(Sk - kt0, (uint32_t)(p.k_ss * 2), D * 2));
+        const auto rv = make_rsrc(vbase + (int64_t)kt0 * p.v_ss, tile_bytes<kBN>(Sk - kt0, (uint32_t)(p.v_ss * 2), D * 2));
 #pragma unroll
         for (int it = 0; it < C::KT; it++) {
             kreg[it] = buffer_load_h8(rk, koff[it], 0);
