@@ -1,7 +1,7 @@
 """CPU oracle for the FlashAttention-2 forward path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
-import this package, and only as the checker.  The shipped library
+import this package, and only to check results against.  The shipped library
 (``rdnattention_amd``) never imports it and has no CPU fallback.
 
 This module is a thin numpy/ctypes layer over ``attn_oracle.c`` (built by

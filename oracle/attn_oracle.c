@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the shipped library links, loads or
  * calls this file; only tests/, __graft_entry__.smoke() and bench.py's CPU
- * baseline use it, and only as the checker.  It restates, in plain C, the
+ * baseline use it, and only to check results against.  It restates, in plain C, the
  * semantics of the reference's attention path (dmonkman/RDNAttention):
  *
  *   - masking        src/rdna/fa2_forward_f16.hip:297-348 (kvBlockRange, isMasked),
