@@ -66,6 +66,7 @@ class Workload:
     seed: int
     std: float
     kernel: str      # the main kernel, as rocprofv3 names it
+    v_token: bool = False  # int8: V quantised per token, dequantised in the kernel
 
     @property
     def flops(self) -> int:
@@ -81,6 +82,8 @@ class Workload:
             n += 2 * max(self.sq, self.sk) * (self.d // 2) * 4
         if self.kind == "int8":
             n += 4 * self.b * (self.hq * self.sq + self.hkv * self.sk)
+        if self.v_token:
+            n += 4 * self.b * self.hkv * self.sk
         return n
 
 
@@ -91,6 +94,8 @@ WORKLOADS = {
         Workload("f16", 1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0, "fa_fwd_f16_pp<64>"),
     "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128":
         Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128>"),
+    "int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128":
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, true>", True),
     "fp16_causal_gqa_b2_h32_kv8_s8192_d128":
         Workload("f16", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<128>"),
     "fp16_decode_b16_h32_kv8_sq1_sk32768_d128":
@@ -105,6 +110,7 @@ WORKLOADS = {
 DEFAULT = "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128"
 SECONDARY = [
     "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128",
+    "int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128",
     "fp16_causal_gqa_b2_h32_kv8_s8192_d128",
     "fp16_decode_b16_h32_kv8_sq1_sk32768_d128",
     "fp16_decode_b16_h32_kv8_sq4_sk32768_d128",
@@ -219,11 +225,16 @@ def make_step(wl: Workload, dev, host=None):
         kf = randn(wl.b, wl.hkv, wl.sk, wl.d)
         vf = randn(wl.b, wl.hkv, wl.sk, wl.d)
         qi, ki, q_scale, k_scale = ra.quantize_int8_qk_pertoken(qf, kf)
-        _, _, vi, _, _, v_scale, _ = ra.quantize_int8_perchannel_v(qf, kf, vf)
+        if wl.v_token:
+            vi, v_tok = ra.quantize_int8_pertoken_v(vf)
+            v_scale = 1.0
+        else:
+            _, _, vi, _, _, v_scale, _ = ra.quantize_int8_perchannel_v(qf, kf, vf)
+            v_tok = None
         del qf, kf, vf
         out = torch.empty(qi.shape, dtype=torch.float16, device=dev)
         return lambda: ra.attention_int8_forward_into(qi, ki, vi, out, q_scale, k_scale, v_scale,
-                                                      is_causal=wl.causal, window_size=wl.window)
+                                                      is_causal=wl.causal, window_size=wl.window, v_token=v_tok)
     if wl.kind == "decode":
         # K/V are views of one [B, S, 2, Hkv, D] cache: head stride D, seq stride 2*Hkv*D
         cache = randn(wl.b, wl.sk, 2, wl.hkv, wl.d).half()
@@ -341,7 +352,7 @@ def profiled_traffic(name: str, wl: Workload):
     """HBM bytes per launch of the workload's main kernel, from the committed
     rocprofv3 counter summary profiles/<kernel>__<workload>.md (its
     "traffic_bytes_per_launch:" line), or None when there is none."""
-    kern = re.sub(r"[<>]", "_", wl.kernel).strip("_")
+    kern = re.sub(r"[<>, ]+", "_", wl.kernel).strip("_")
     path = ROOT / "profiles" / f"{kern}__{name}.md"
     try:
         text = path.read_text()
@@ -540,6 +551,9 @@ def main(argv=None):
         f16 = secondary.get("fp16_causal_gqa_b2_h32_kv8_s8192_d128", {})
         if "kernel_ms" in i8 and "kernel_ms" in f16:
             secondary["int8_over_fp16_same_shape"] = round(f16["kernel_ms"] / i8["kernel_ms"], 3)
+        i8t = secondary.get("int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128", {})
+        if "kernel_ms" in i8 and "kernel_ms" in i8t:
+            secondary["int8_vtoken_time_over_int8"] = round(i8t["kernel_ms"] / i8["kernel_ms"], 3)
         try:
             secondary["int8_quantized_end_to_end"] = int8_quantized_e2e(dev)
         except ra.RDNAttentionError as e:

@@ -62,6 +62,28 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
     const void* q_scale_vec, const void* k_scale_vec, const void* v_channel_vec,
     int32_t causal, int32_t window_size, void* hip_stream);
 
+/* rdna_attention_forward_int8qk() with a per-token V scale: V row j of each
+ * (batch, kv head) is dequantised by v_token_vec[b, kv_head, j] while the
+ * kernel stages it, v'_j = fp16(v_i8[j] * v_token_vec[...]), and the
+ * quantised P (the reference's pq = min(127, round(127 p))) multiplies these
+ * fp16 rows: output = sum_j pq_j v'_j * v_scale / (127 l).  v_token_vec is a
+ * contiguous fp32 [batch, num_kv_heads, key_seq_len] device array (4-byte
+ * aligned, required).  No reference counterpart: the reference lists a
+ * per-token V scale as missing (FEATURES.md:191, :201-202); this is the extension
+ * that fills it, with the per-token V quantiser of
+ * quantize_int8_qk_pertoken's formula. */
+RDNA_API int32_t rdna_attention_forward_int8qk_vtoken(
+    const void* q, const void* k, const void* v, void* output,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads,
+    uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
+    float scale, float q_scale, float k_scale, float v_scale,
+    const void* q_scale_vec, const void* k_scale_vec, const void* v_token_vec,
+    int32_t causal, int32_t window_size, void* hip_stream);
+
 /* INT8 quantisation on the GPU, bit-identical to the reference wrapper's
  * torch ops (rdnattention/__init__.py:303-343):
  *   per_channel == 0 (per token): scale[b,h,s] = max_d |x| / 127 (0 -> 1)

@@ -63,6 +63,11 @@ def lib():
                                             ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_int32]
         L.oracle_attention_int8.restype = ctypes.c_int32
+        L.oracle_attention_int8_vtoken.argtypes = [_i8p, _i8p, _i8p, _f32p, _f32p, _f32p, ctypes.c_float,
+                                                   ctypes.c_float, ctypes.c_float, _f32p, _i64, _i64, _i64, _i64,
+                                                   _i64, _i64, ctypes.c_float, ctypes.c_int32, ctypes.c_int32,
+                                                   ctypes.c_int32, ctypes.c_int32]
+        L.oracle_attention_int8_vtoken.restype = ctypes.c_int32
         L.oracle_attention_int8_gate.argtypes = [_f32p, _f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _i64,
                                                  ctypes.c_double, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
         L.oracle_attention_int8_gate.restype = ctypes.c_int32
@@ -195,8 +200,10 @@ def int8_scores(qi, ki):
 
 
 def attention_int8(qi, ki, vi, q_scale, k_scale, v_scale, causal=False, window=-1, scale=None, block_n=64,
-                   nthreads=None):
-    """Kernel-exact INT8 emulation.  q_scale / k_scale: float or per-token array."""
+                   nthreads=None, v_token=None):
+    """Kernel-exact INT8 emulation.  q_scale / k_scale: float or per-token array.
+    v_token: per-token V scales [B, Hkv, Sk] (the library's extension; V row j
+    becomes fp16(fp32(v_j) * v_token_j) before P V), or None."""
     qi = _c(qi, np.int8)
     ki = _c(ki, np.int8)
     vi = _c(vi, np.int8)
@@ -207,6 +214,21 @@ def attention_int8(qi, ki, vi, q_scale, k_scale, v_scale, causal=False, window=-
     qsv = _c(q_scale, np.float32) if isinstance(q_scale, np.ndarray) else None
     ksv = _c(k_scale, np.float32) if isinstance(k_scale, np.ndarray) else None
     out = np.empty((b, hq, sq, d), dtype=np.float32)
+    if v_token is not None:
+        vtv = _c(v_token, np.float32)
+        if vtv.shape != (b, hkv, sk):
+            raise ValueError(f"v_token shape {vtv.shape} != {(b, hkv, sk)}")
+        rc = lib().oracle_attention_int8_vtoken(_p(qi, _i8p), _p(ki, _i8p), _p(vi, _i8p),
+                                                _p(qsv, _f32p) if qsv is not None else None,
+                                                _p(ksv, _f32p) if ksv is not None else None, _p(vtv, _f32p),
+                                                1.0 if qsv is not None else float(q_scale),
+                                                1.0 if ksv is not None else float(k_scale), float(v_scale),
+                                                _p(out, _f32p), b, hq, hkv, sq, sk, d, float(scale),
+                                                1 if causal else 0, int(window), int(block_n),
+                                                nthreads or default_threads())
+        if rc != 0:
+            raise ValueError(f"oracle_attention_int8_vtoken rc={rc}")
+        return out
     rc = lib().oracle_attention_int8(_p(qi, _i8p), _p(ki, _i8p), _p(vi, _i8p),
                                      _p(qsv, _f32p) if qsv is not None else None,
                                      _p(ksv, _f32p) if ksv is not None else None,

@@ -394,10 +394,13 @@ ORACLE_API int32_t oracle_int8_scores(const int8_t* q, const int8_t* k, int32_t*
 /* arithmetic gives (masked p = 0, max unchanged).                             */
 /* q_scale_vec: [B,Hq,Sq] or NULL (use q_scale); k_scale_vec: [B,Hkv,Sk] or   */
 /* NULL (use k_scale) -- the contiguous indexing of :410 and :287.           */
+/* v_token_vec ([B,Hkv,Sk], the library's per-token V extension; no          */
+/* reference counterpart): V row j becomes v'_j = fp16(fp32(v_j) * vs_j) and */
+/* O += (sum_j pq_j v'_j) * ((1/127) * v_scale), the sum in double.          */
 /* ------------------------------------------------------------------------ */
 typedef struct {
     const int8_t *q, *k, *v;
-    const float *qsv, *ksv;
+    const float *qsv, *ksv, *vtv;
     float qs, ks, vs;
     float* out;
     int64_t B, Hq, Hkv, Sq, Sk, D;
@@ -422,6 +425,8 @@ static void i8_task(void* vctx, int64_t task) {
     float* sj = (float*)malloc(sizeof(float) * (size_t)bn);
     int32_t* pq = (int32_t*)malloc(sizeof(int32_t) * (size_t)bn);
     int32_t* pv = (int32_t*)malloc(sizeof(int32_t) * (size_t)c->D);
+    double* pvd = (double*)malloc(sizeof(double) * (size_t)c->D);
+    const float* vtb = c->vtv ? c->vtv + (b * c->Hkv + kvh) * c->Sk : NULL;
     for (int64_t i = 0; i < c->Sq; i++) {
         float qs = c->qsv ? c->qsv[(b * c->Hq + h) * c->Sq + i] : c->qs;
         float m = -INFINITY, l = 0.0f;
@@ -477,6 +482,7 @@ static void i8_task(void* vctx, int64_t task) {
             m = mnew;
             for (int64_t d = 0; d < c->D; d++) {
                 pv[d] = 0;
+                pvd[d] = 0.0;
             }
             for (int64_t jj = 0; jj < bn; jj++) {
                 int64_t j = k0 + jj;
@@ -484,12 +490,18 @@ static void i8_task(void* vctx, int64_t task) {
                     continue;
                 }
                 const int8_t* vr = vb + j * c->D;
-                for (int64_t d = 0; d < c->D; d++) {
-                    pv[d] += pq[jj] * (int32_t)vr[d];
+                if (vtb) {
+                    for (int64_t d = 0; d < c->D; d++) {
+                        pvd[d] += (double)pq[jj] * (double)oracle_round_f16((float)vr[d] * vtb[j]);
+                    }
+                } else {
+                    for (int64_t d = 0; d < c->D; d++) {
+                        pv[d] += pq[jj] * (int32_t)vr[d];
+                    }
                 }
             }
             for (int64_t d = 0; d < c->D; d++) {
-                o[d] += (float)pv[d] * pvScale;
+                o[d] += (vtb ? (float)pvd[d] : (float)pv[d]) * pvScale;
             }
         }
         float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -501,6 +513,7 @@ static void i8_task(void* vctx, int64_t task) {
     free(sj);
     free(pq);
     free(pv);
+    free(pvd);
 }
 
 ORACLE_API int32_t oracle_attention_int8(const int8_t* q, const int8_t* k, const int8_t* v, const float* q_scale_vec,
@@ -515,8 +528,28 @@ ORACLE_API int32_t oracle_attention_int8(const int8_t* q, const int8_t* k, const
     if (block_n <= 0) {
         return -3;
     }
-    i8_ctx c = {q,  k,  v,  q_scale_vec, k_scale_vec, q_scale, k_scale, v_scale, out,   B,
-                Hq, Hkv, Sq, Sk,         D,           scale,   causal != 0, window, block_n};
+    i8_ctx c = {q,  k,  v,  q_scale_vec, k_scale_vec, NULL,   q_scale, k_scale, v_scale, out,
+                B,  Hq, Hkv, Sq,         Sk,          D,      scale,   causal != 0, window, block_n};
+    run_tasks(i8_task, &c, B * Hq, nthreads);
+    return 0;
+}
+
+/* oracle_attention_int8 with a per-token V scale v_token_vec [B,Hkv,Sk]. */
+ORACLE_API int32_t oracle_attention_int8_vtoken(const int8_t* q, const int8_t* k, const int8_t* v,
+                                                const float* q_scale_vec, const float* k_scale_vec,
+                                                const float* v_token_vec, float q_scale, float k_scale, float v_scale,
+                                                float* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                                                int64_t D, float scale, int32_t causal, int32_t window,
+                                                int32_t block_n, int32_t nthreads) {
+    int rc = check_dims(B, Hq, Hkv, Sq, Sk, D);
+    if (rc) {
+        return rc;
+    }
+    if (block_n <= 0 || v_token_vec == NULL) {
+        return -3;
+    }
+    i8_ctx c = {q,  k,  v,  q_scale_vec, k_scale_vec, v_token_vec, q_scale, k_scale, v_scale, out,
+                B,  Hq, Hkv, Sq,         Sk,          D,           scale,   causal != 0, window, block_n};
     run_tasks(i8_task, &c, B * Hq, nthreads);
     return 0;
 }

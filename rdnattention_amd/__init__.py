@@ -88,6 +88,8 @@ def _lib_handle():
         lib.rdna_attention_forward_int8qk.restype = _I32
         lib.rdna_attention_forward_int8qk_vchannel.argtypes = _I8_ARGS[:-3] + [_VP] + _I8_ARGS[-3:]
         lib.rdna_attention_forward_int8qk_vchannel.restype = _I32
+        lib.rdna_attention_forward_int8qk_vtoken.argtypes = _I8_ARGS[:-3] + [_VP] + _I8_ARGS[-3:]
+        lib.rdna_attention_forward_int8qk_vtoken.restype = _I32
         lib.rdna_quantize_int8.argtypes = [_VP, _I32] + [_I64] * 3 + [_U32] * 4 + [_I32, _VP, _VP, _VP, _VP, _VP]
         lib.rdna_quantize_int8.restype = _I32
         lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
@@ -300,7 +302,7 @@ def flash_attn_int8qk(query, key, value, q_scale, k_scale, v_scale: float, is_ca
 
 def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_scale: float, *,
                                 is_causal: bool = False, window_size: int = -1, scale=None,
-                                v_channel=None) -> None:
+                                v_channel=None, v_token=None) -> None:
     """INT8 forward written into a preallocated float16 `output` (the raw
     rdna_attention_forward_int8qk call, src/c_api.cpp:116-195).
 
@@ -310,8 +312,11 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
     tensors of per-token scales [batch, heads, seq_len] /
     [batch, kv_heads, key_seq_len].  v_channel: optional contiguous float32
     device tensor [batch, kv_heads, head_dim] of per-channel V scales applied
-    in the kernel (rdna_attention_forward_int8qk_vchannel).  Asynchronous on
-    torch's current stream."""
+    in the kernel (rdna_attention_forward_int8qk_vchannel).  v_token:
+    optional contiguous float32 device tensor [batch, kv_heads, key_seq_len]
+    of per-token V scales, each V row dequantised by its own scale in the
+    kernel (rdna_attention_forward_int8qk_vtoken; exclusive with v_channel).
+    Asynchronous on torch's current stream."""
     import torch
 
     for name, t in (("query", query), ("key", key), ("value", value)):
@@ -338,7 +343,15 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
             float(head_dim ** -0.5 if scale is None else scale), q_scalar, k_scalar, float(v_scale),
             q_vec.data_ptr() if q_vec is not None else None, k_vec.data_ptr() if k_vec is not None else None]
     tail = [1 if is_causal else 0, int(window_size), _stream()]
-    if v_channel is None:
+    if v_channel is not None and v_token is not None:
+        raise ValueError("pass v_channel or v_token, not both")
+    if v_token is not None:
+        want = (batch, kv_heads, key_seq_len)
+        if (not isinstance(v_token, torch.Tensor) or v_token.dtype != torch.float32
+                or not v_token.is_contiguous() or tuple(v_token.shape) != want or not v_token.is_cuda):
+            raise ValueError(f"v_token must be a contiguous float32 HIP tensor of shape {want}")
+        result = _lib_handle().rdna_attention_forward_int8qk_vtoken(*args, v_token.data_ptr(), *tail)
+    elif v_channel is None:
         result = _lib_handle().rdna_attention_forward_int8qk(*args, *tail)
     else:
         want = (batch, kv_heads, head_dim)
@@ -492,8 +505,23 @@ def quantize_int8_qk_pertoken(query, key, rot_cos=None, rot_sin=None):
     return qi, ki, q_scale, k_scale
 
 
+def quantize_int8_pertoken_v(value):
+    """(vi, v_token): V quantised with one fp32 scale per (batch, head, row),
+    the per-token formula of quantize_int8_qk_pertoken (an extension; the
+    reference has no per-token V scale).  Use with attention_int8_forward_into
+    (v_token=...) or flash_attn_int8qk_quantized(v_per_token=True)."""
+    import torch
+
+    if value.is_cuda:
+        return _quantize_gpu(value, per_channel=False)
+    x = value.float()
+    s = x.abs().amax(dim=-1, keepdim=True) / 127.0
+    s = torch.where(s == 0, torch.ones_like(s), s)
+    return torch.clamp(torch.round(x / s), -127, 127).to(torch.int8), s.squeeze(-1).contiguous()
+
+
 def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, window_size: int = -1, rot_cos=None,
-                                rot_sin=None):
+                                rot_sin=None, v_per_token: bool = False):
     """INT8 attention from ordinary fp16/fp32 Q/K/V (rdnattention/__init__.py:346-357):
     per-token Q/K scales and a per-channel V scale.
 
@@ -511,7 +539,11 @@ def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, wind
 
     Differs from the reference in one more respect: v_channel is indexed by
     the kv head of each query head, so grouped-query inputs with
-    1 < kv_heads < heads work (the reference's broadcast raises there)."""
+    1 < kv_heads < heads work (the reference's broadcast raises there).
+
+    v_per_token (an extension): V is quantised per token instead of per
+    channel, and the kernel dequantises each V row by its scale
+    (rdna_attention_forward_int8qk_vtoken)."""
     import torch
 
     for name, t in (("query", query), ("key", key), ("value", value)):
@@ -533,12 +565,13 @@ def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, wind
     _rope_ptrs(rot_cos, rot_sin, query, query.shape[2], key.shape[2], query.shape[3])
     qi, q_scale = _quantize_gpu(query, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
     ki, k_scale = _quantize_gpu(key, per_channel=False, rot_cos=rot_cos, rot_sin=rot_sin)
-    vi, v_channel = _quantize_gpu(value, per_channel=True)
+    vi, v_sc = _quantize_gpu(value, per_channel=not v_per_token)
     output = torch.empty(query.shape, dtype=torch.float16, device=query.device)
     if output.numel() == 0:
         return output
     attention_int8_forward_into(qi, ki, vi, output, q_scale, k_scale, 1.0, is_causal=is_causal,
-                                window_size=window_size, v_channel=v_channel)
+                                window_size=window_size, v_channel=None if v_per_token else v_sc,
+                                v_token=v_sc if v_per_token else None)
     return output
 
 

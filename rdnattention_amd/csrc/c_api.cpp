@@ -127,7 +127,7 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
                         int64_t osb, int64_t osh, int64_t oss, uint32_t B, uint32_t Hq, uint32_t Hkv, uint32_t Sq,
                         uint32_t Sk, uint32_t D, float scale, float q_scale, float k_scale, float v_scale,
                         const void* q_scale_vec, const void* k_scale_vec, const void* v_channel_vec,
-                        int32_t causal, int32_t window, void* stream, std::string& err) {
+                        const void* v_token_vec, int32_t causal, int32_t window, void* stream, std::string& err) {
     // order of the reference's checks: ratio, then head_dim (fa2_forward_int8qk.hip:570-589)
     if (Hkv == 0 || Hq % Hkv != 0) {
         err = "numHeads must be a positive multiple of numKvHeads";
@@ -158,6 +158,14 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
         err = "v_channel_vec must be a 16-byte aligned float array";
         return -1;
     }
+    if (!aligned(v_token_vec, 4)) {
+        err = "v_token_vec must be a 4-byte aligned float array";
+        return -1;
+    }
+    if (v_channel_vec != nullptr && v_token_vec != nullptr) {
+        err = "v_channel_vec and v_token_vec are exclusive";
+        return -1;
+    }
     a.B = (int32_t)B;
     a.Hq = (int32_t)Hq;
     a.Hkv = (int32_t)Hkv;
@@ -173,6 +181,7 @@ int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* outpu
     a.q_scale_vec = static_cast<const float*>(q_scale_vec);
     a.k_scale_vec = static_cast<const float*>(k_scale_vec);
     a.v_channel = static_cast<const float*>(v_channel_vec);
+    a.v_token = static_cast<const float*>(v_token_vec);
     return rdna_amd::fwd_int8(a, static_cast<hipStream_t>(stream), err);
 }
 
@@ -257,7 +266,7 @@ RDNA_API int32_t rdna_attention_forward_int8qk(const void* q, const void* k, con
     int rc = forward_i8_impl(q, k, v, output, q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s,
                              v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h, o_stride_s, batch_size,
                              num_heads, num_kv_heads, seq_len, key_seq_len, head_dim, scale, q_scale, k_scale,
-                             v_scale, q_scale_vec, k_scale_vec, nullptr, causal, window_size, hip_stream, err);
+                             v_scale, q_scale_vec, k_scale_vec, nullptr, nullptr, causal, window_size, hip_stream, err);
     if (rc != 0) {
         set_error("Attention (int8qk) failed: %s", err);
         return -3;
@@ -287,7 +296,43 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
     int rc = forward_i8_impl(q, k, v, output, q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s,
                              v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h, o_stride_s, batch_size,
                              num_heads, num_kv_heads, seq_len, key_seq_len, head_dim, scale, q_scale, k_scale,
-                             v_scale, q_scale_vec, k_scale_vec, v_channel_vec, causal, window_size, hip_stream, err);
+                             v_scale, q_scale_vec, k_scale_vec, v_channel_vec, nullptr, causal, window_size,
+                             hip_stream, err);
+    if (rc != 0) {
+        set_error("Attention (int8qk) failed: %s", err);
+        return -3;
+    }
+    return 0;
+#endif
+}
+
+RDNA_API int32_t rdna_attention_forward_int8qk_vtoken(
+    const void* q, const void* k, const void* v, void* output, int64_t q_stride_b, int64_t q_stride_h,
+    int64_t q_stride_s, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s, int64_t v_stride_b,
+    int64_t v_stride_h, int64_t v_stride_s, int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads, uint32_t seq_len, uint32_t key_seq_len,
+    uint32_t head_dim, float scale, float q_scale, float k_scale, float v_scale, const void* q_scale_vec,
+    const void* k_scale_vec, const void* v_token_vec, int32_t causal, int32_t window_size, void* hip_stream) {
+#if defined(RDNATTENTION_NO_INT8)
+    (void)q, (void)k, (void)v, (void)output, (void)q_stride_b, (void)q_stride_h, (void)q_stride_s;
+    (void)k_stride_b, (void)k_stride_h, (void)k_stride_s, (void)v_stride_b, (void)v_stride_h, (void)v_stride_s;
+    (void)o_stride_b, (void)o_stride_h, (void)o_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads;
+    (void)seq_len, (void)key_seq_len, (void)head_dim, (void)scale, (void)q_scale, (void)k_scale, (void)v_scale;
+    (void)q_scale_vec, (void)k_scale_vec, (void)v_token_vec, (void)causal, (void)window_size, (void)hip_stream;
+    set_error("Attention (int8qk) unavailable: %s",
+              "this library was built without the INT8 kernel - use rdna_attention_forward() instead");
+    return -4;
+#else
+    if (v_token_vec == nullptr) {
+        set_error("Attention (int8qk) failed: %s", std::string("v_token_vec is null"));
+        return -3;
+    }
+    std::string err;
+    int rc = forward_i8_impl(q, k, v, output, q_stride_b, q_stride_h, q_stride_s, k_stride_b, k_stride_h, k_stride_s,
+                             v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h, o_stride_s, batch_size,
+                             num_heads, num_kv_heads, seq_len, key_seq_len, head_dim, scale, q_scale, k_scale,
+                             v_scale, q_scale_vec, k_scale_vec, nullptr, v_token_vec, causal, window_size,
+                             hip_stream, err);
     if (rc != 0) {
         set_error("Attention (int8qk) failed: %s", err);
         return -3;
@@ -416,8 +461,8 @@ int forwardInt8QK(const ForwardParamsInt8QK& p, void* stream) {
     int rc = forward_i8_impl(p.q, p.k, p.v, p.o, p.qStrideB, p.qStrideH, p.qStrideS, p.kStrideB, p.kStrideH,
                              p.kStrideS, p.vStrideB, p.vStrideH, p.vStrideS, p.oStrideB, p.oStrideH, p.oStrideS,
                              p.batchSize, p.numHeads, p.numKvHeads, p.seqLen, p.keySeqLen, p.headDim, p.scale,
-                             p.qScale, p.kScale, p.vScale, p.qScaleVec, p.kScaleVec, nullptr, (int32_t)p.causal,
-                             p.windowSize, stream, err);
+                             p.qScale, p.kScale, p.vScale, p.qScaleVec, p.kScaleVec, nullptr, nullptr,
+                             (int32_t)p.causal, p.windowSize, stream, err);
     if (rc != 0) {
         std::snprintf(g_last_i8, sizeof(g_last_i8), "%s", err.c_str());
         return -1;

@@ -59,6 +59,7 @@ struct Int8Params {
     const float* qsv; // [B, Hq, Sq] or null
     const float* ksv; // [B, Hkv, Sk] or null
     const float* vch; // [B, Hkv, D] per-channel V scale or null
+    const float* vtok; // [B, Hkv, Sk] per-token V scale (the VTOK kernel) or null
     float q_scale, k_scale;
     float v_scale;
     float scale_log2e;
@@ -109,6 +110,18 @@ __device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
     }
 }
 
+// 16 signed bytes of one V row -> two h8 of fp16(v * vs), the product rounded
+// once from fp32
+__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, float vs, h8& lo, h8& hi) {
+    const i8x8 a = __builtin_bit_cast(i8x8, i2{w[0], w[1]});
+    const i8x8 b = __builtin_bit_cast(i8x8, i2{w[2], w[3]});
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        lo[e] = (_Float16)((float)a[e] * vs);
+        hi[e] = (_Float16)((float)b[e] * vs);
+    }
+}
+
 // Scheme (the reference's, fa2_forward_int8qk.hip:281-382), per 64-key block b
 // aligned to key 0, with s_j = S_j * qs * ks_j * scale * log2(e):
 //   m_b  = max(m_{b-1}, max_j s_j),  corr = 2^(m_{b-1} - m_b)
@@ -120,7 +133,11 @@ __device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
 // S runs on int8 MFMA (exact int32).  P V runs on fp16 MFMA, which is exact
 // for these integer operands and accumulates straight into fp32, so O needs
 // no per-block int32 -> fp32 conversion.
-template <int D>
+//
+// VTOK (an extension; the reference has no per-token V scale): V row j is
+// dequantised by its own scale vs_j while it is staged, v'_j = fp16(v_j * vs_j),
+// and P V runs on these fp16 values: O = O * corr + sum_j pq_j v'_j.
+template <int D, bool VTOK>
 __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     using C = I8Cfg<D>;
     __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
@@ -162,6 +179,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         const int8_t* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
         _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
         const float* ksbase = p.ksv ? p.ksv + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
+        const float* vtbase = VTOK ? p.vtok + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
 
         // Q^T operand: lane holds Q[q][32s + 16g .. +15]
         i4 qreg[C::NS];
@@ -227,6 +245,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             clv[it] = ok ? row * C::LDV + 16 * ch : -1;
         }
         float ksreg = 0.0f;
+        float vsreg[C::CT]; // VTOK: the scale of each staged V row
         auto load_pair = [&](int x) {
             const int tk = t_begin + x, tv = t_begin + x - 1;
             const auto rk = make_rsrc(kbase + (int64_t)tk * kI8BN * p.k_ss,
@@ -237,6 +256,10 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             for (int it = 0; it < C::CT; it++) {
                 kreg[it] = buffer_load_i4(rk, coff_k[it]);
                 vreg[it] = buffer_load_i4(rv, coff_v[it]);
+                if constexpr (VTOK) {
+                    const int key = tv * kI8BN + 32 * grp + (gtid + it * 256) / C::KCH;
+                    vsreg[it] = (x >= 1 && x <= n && key < Sk) ? vtbase[key] : 0.0f;
+                }
             }
             if (grp == 0 && gtid < kI8BN && x < n) {
                 const int key = tk * kI8BN + gtid;
@@ -254,7 +277,11 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     }
                     if (x >= 1 && x <= n) {
                         h8 lo, hi;
-                        i8x16_to_h8x2(vreg[it], lo, hi);
+                        if constexpr (VTOK) {
+                            i8x16_to_h8x2_scaled(vreg[it], vsreg[it], lo, hi);
+                        } else {
+                            i8x16_to_h8x2(vreg[it], lo, hi);
+                        }
                         *reinterpret_cast<h8*>(&sV[clv[it]]) = lo;
                         *reinterpret_cast<h8*>(&sV[clv[it] + 8]) = hi;
                     }
@@ -509,17 +536,18 @@ __global__ __launch_bounds__(64) void int8_scores_kernel(const int8_t* __restric
     }
 }
 
-template <int D>
+template <int D, bool VTOK>
 int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     // persistent: as many workgroups as the device holds at once, each
     // walking its share of the n_wg row tiles
-    const int64_t resident = resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D>), kI8Threads, err);
+    const int64_t resident =
+        resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D, VTOK>), kI8Threads, err);
     if (resident <= 0) {
         return -1;
     }
     const int64_t grid = std::min(n_wg, resident);
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_int8<D>, dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
+    hipLaunchKernelGGL((fa_fwd_int8<D, VTOK>), dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -543,6 +571,7 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     p.qsv = a.q_scale_vec;
     p.ksv = a.k_scale_vec;
     p.vch = a.v_channel;
+    p.vtok = a.v_token;
     p.q_scale = a.q_scale;
     p.k_scale = a.k_scale;
     p.v_scale = a.v_scale;
@@ -577,8 +606,9 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     }
     p.n_items = (int32_t)n_wg;
     switch (a.D) {
-    case 64: return launch_int8<64>(p, n_wg, stream, err);
-    case 128: return launch_int8<128>(p, n_wg, stream, err);
+    case 64: return p.vtok ? launch_int8<64, true>(p, n_wg, stream, err) : launch_int8<64, false>(p, n_wg, stream, err);
+    case 128:
+        return p.vtok ? launch_int8<128, true>(p, n_wg, stream, err) : launch_int8<128, false>(p, n_wg, stream, err);
     default: break;
     }
     err = "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)";

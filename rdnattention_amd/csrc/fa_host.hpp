@@ -34,6 +34,9 @@ struct AttnArgs {
     // per-channel V scale [B, Hkv, D] (contiguous) multiplied into the output,
     // or null
     const float* v_channel = nullptr;
+    // per-token V scale [B, Hkv, Sk] (contiguous) applied to each V row as it
+    // is staged, or null
+    const float* v_token = nullptr;
 };
 
 // INT8 quantiser arguments: x fp16 or fp32 [B, H, S, D] (element strides

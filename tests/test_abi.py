@@ -141,6 +141,26 @@ def test_int8_argument_errors(lib, kw, msg):
     assert msg in err
 
 
+def test_int8_vtoken_argument_errors(lib):
+    """rdna_attention_forward_int8qk_vtoken: the scale array is required, 4-byte
+    aligned, and checked before any HIP call."""
+    import rdnattention_amd
+
+    rdnattention_amd._lib_handle()
+    hold, p = _buf()
+    s = (8 * 8 * 64, 8 * 64, 64)
+
+    def call(vt):
+        rc = lib.rdna_attention_forward_int8qk_vtoken(p, p, p, p, *s, *s, *s, *s, 1, 8, 8, 8, 8, 64, 0.125, 1.0,
+                                                      1.0, 1.0, None, None, vt, 0, -1, None)
+        return rc, lib.rdna_get_error().decode()
+
+    rc, err = call(None)
+    assert rc == -3 and "v_token_vec is null" in err
+    rc, err = call(p + 2)
+    assert rc == -3 and "v_token_vec must be a 4-byte aligned" in err
+
+
 def test_has_device_without_gpu(lib):
     import torch
 

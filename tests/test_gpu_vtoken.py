@@ -1,0 +1,127 @@
+"""Per-token V scale (rdna_attention_forward_int8qk_vtoken; an extension: the
+reference lists a per-token V scale as missing, FEATURES.md:191, :201-202).
+
+* Exact rows: per-token scales in {1, 2, 4} on V values in [-31, 31] dequantise
+  to exact integers, so the kernel must give bit for bit what the plain INT8
+  kernel gives on the pre-multiplied V.
+* Real scales: within 1e-2 max-abs of the oracle's kernel-exact emulation
+  (oracle.attention_int8(..., v_token=...)).
+* End to end: flash_attn_int8qk_quantized(v_per_token=True) against the
+  emulation on the same GPU-quantised tensors, and against fp attention.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.gpu_util import I8_MAX_ABS, errors, log
+
+# name, B, Hq, Hkv, Sq, Sk, D, causal, window, per-token Q/K, strided V
+CASES = [
+    ("d128_gqa_causal", 2, 8, 2, 300, 300, 128, True, -1, True, False),
+    ("d64_window", 1, 4, 4, 256, 256, 64, False, 64, False, False),
+    ("d128_kv_longer", 1, 4, 1, 64, 500, 128, True, -1, True, False),
+    ("d64_strided_v", 2, 4, 2, 200, 200, 64, True, -1, True, True),
+    ("d128_decode", 2, 8, 2, 1, 1000, 128, True, -1, True, False),
+]
+
+
+def _device_v(v_np, strided):
+    v = torch.from_numpy(v_np).cuda()
+    if not strided:
+        return v
+    b, h, s, d = v.shape
+    big = torch.zeros((b, s, h + 1, d + 32), dtype=torch.int8, device="cuda")
+    view = big[:, :, 1:, 16:16 + d].permute(0, 2, 1, 3)
+    view.copy_(v)
+    return view
+
+
+def _scales(case, rng):
+    name, b, hq, hkv, sq, sk, d, causal, window, ptok, strided = case
+    if ptok:
+        qs = rng.uniform(0.002, 0.01, (b, hq, sq)).astype(np.float32)
+        ks = rng.uniform(0.002, 0.01, (b, hkv, sk)).astype(np.float32)
+        return qs, ks
+    return 0.004, 0.006
+
+
+def _run(qi, ki, vi, qs, ks, causal, window, v_token=None):
+    import rdnattention_amd as ra
+
+    out = torch.full(qi.shape, float("nan"), dtype=torch.float16, device="cuda")
+    dq = torch.from_numpy(qs).cuda() if isinstance(qs, np.ndarray) else qs
+    dk = torch.from_numpy(ks).cuda() if isinstance(ks, np.ndarray) else ks
+    vt = torch.from_numpy(v_token).cuda() if v_token is not None else None
+    ra.attention_int8_forward_into(qi, ki, vi, out, dq, dk, 1.0, is_causal=causal, window_size=window, v_token=vt)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_vtoken_exact_rows_bit_identical(gpu, case):
+    name, b, hq, hkv, sq, sk, d, causal, window, ptok, strided = case
+    log(f"vtoken exact {name}")
+    rng = np.random.default_rng(71)
+    qi = rng.integers(-127, 128, (b, hq, sq, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (b, hkv, sk, d), dtype=np.int8)
+    w = rng.integers(-31, 32, (b, hkv, sk, d), dtype=np.int8)
+    vs = rng.choice(np.array([1.0, 2.0, 4.0], np.float32), size=(b, hkv, sk))
+    v_full = (w.astype(np.int32) * vs[..., None].astype(np.int32)).astype(np.int8)
+    qs, ks = _scales(case, rng)
+    dq, dk = torch.from_numpy(qi).cuda(), torch.from_numpy(ki).cuda()
+    a = _run(dq, dk, _device_v(w, strided), qs, ks, causal, window, v_token=vs)
+    ref = _run(dq, dk, _device_v(v_full, strided), qs, ks, causal, window)
+    assert torch.isfinite(a.float()).all(), name
+    assert torch.equal(a.view(torch.int16), ref.view(torch.int16)), name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_vtoken_vs_emulation(gpu, case):
+    name, b, hq, hkv, sq, sk, d, causal, window, ptok, strided = case
+    log(f"vtoken emulation {name}")
+    rng = np.random.default_rng(72)
+    qi = rng.integers(-127, 128, (b, hq, sq, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (b, hkv, sk, d), dtype=np.int8)
+    vi = rng.integers(-127, 128, (b, hkv, sk, d), dtype=np.int8)
+    vt = rng.uniform(0.001, 0.03, (b, hkv, sk)).astype(np.float32)
+    qs, ks = _scales(case, rng)
+    got = _run(torch.from_numpy(qi).cuda(), torch.from_numpy(ki).cuda(), _device_v(vi, strided), qs, ks, causal,
+               window, v_token=vt)
+    ref = oracle.attention_int8(qi, ki, vi, qs, ks, 1.0, causal=causal, window=window, v_token=vt)
+    mx, mean, rel = errors(got.float().cpu().numpy(), ref)
+    log(f"  max_abs={mx:.3e} mean_abs={mean:.3e} rel_rms={rel:.3e}")
+    assert mx <= I8_MAX_ABS, (name, mx)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_vtoken_quantized_end_to_end(gpu, causal):
+    import rdnattention_amd as ra
+
+    log(f"vtoken end to end causal={causal}")
+    g = torch.Generator().manual_seed(73)
+    b, hq, hkv, s, d = 1, 8, 2, 400, 128
+    q = torch.randn(b, hq, s, d, generator=g).half()
+    k = torch.randn(b, hkv, s, d, generator=g).half()
+    v = torch.randn(b, hkv, s, d, generator=g).half()
+    out = ra.flash_attn_int8qk_quantized(q.cuda(), k.cuda(), v.cuda(), is_causal=causal, v_per_token=True)
+    torch.cuda.synchronize()
+    qi, ki, qs, ks = ra.quantize_int8_qk_pertoken(q.cuda(), k.cuda())
+    vi, vt = ra.quantize_int8_pertoken_v(v.cuda())
+    # the GPU quantiser equals the reference's per-token torch formula on the same device tensor
+    from tests.test_gpu_quant import torch_pertoken
+
+    ti, ts = torch_pertoken(v.cuda())
+    assert torch.equal(vi, ti) and torch.equal(vt, ts)
+    ref = oracle.attention_int8(qi.cpu().numpy(), ki.cpu().numpy(), vi.cpu().numpy(), qs.cpu().numpy(),
+                                ks.cpu().numpy(), 1.0, causal=causal, v_token=vt.cpu().numpy())
+    mx, mean, rel = errors(out.float().cpu().numpy(), ref)
+    log(f"  vs emulation max_abs={mx:.3e}")
+    assert mx <= I8_MAX_ABS
+    fp = oracle.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal)
+    mx, mean, rel = errors(out.float().cpu().numpy(), fp)
+    log(f"  vs fp attention rel_rms={rel:.3e}")
+    assert rel < 5e-2

@@ -383,6 +383,61 @@ def test_int8_blockwise_depends_on_running_max(oracle_lib):
     np.testing.assert_array_equal(c, d)
 
 
+def _vtoken_exact_inputs(seed, b, hq, hkv, sq, sk, d):
+    """Per-token V inputs whose dequantised rows are exact integers: w in
+    [-31, 31], vs in {1, 2, 4} per (batch, kv head, row), so w * vs is an int8
+    value and fp16(w * vs) = w * vs."""
+    rng = np.random.default_rng(seed)
+    qi = rng.integers(-127, 128, (b, hq, sq, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (b, hkv, sk, d), dtype=np.int8)
+    w = rng.integers(-31, 32, (b, hkv, sk, d), dtype=np.int8)
+    vs = rng.choice(np.array([1.0, 2.0, 4.0], np.float32), size=(b, hkv, sk))
+    v_full = (w.astype(np.int32) * vs[..., None].astype(np.int32)).astype(np.int8)
+    return qi, ki, w, vs, v_full
+
+
+def test_int8_vtoken_exact_rows_equal_per_tensor_path(oracle_lib):
+    """Per-token V scales that dequantise to exact integers must give exactly
+    the per-tensor result on the pre-multiplied V: pins the row indexing of
+    v_token per (batch, kv head, key) and the sum itself (a wrong row, head
+    or batch offset would mix the {1, 2, 4} factors)."""
+    qi, ki, w, vs, v_full = _vtoken_exact_inputs(61, 2, 4, 2, 40, 150, 64)
+    a = oracle_lib.attention_int8(qi, ki, w, 0.004, 0.006, 1.0, causal=True, v_token=vs)
+    b = oracle_lib.attention_int8(qi, ki, v_full, 0.004, 0.006, 1.0, causal=True)
+    np.testing.assert_array_equal(a, b)
+    c = oracle_lib.attention_int8(qi, ki, w, 0.004, 0.006, 1.0, causal=True, v_token=vs[:, ::-1].copy())
+    assert not np.array_equal(a, c)  # the kv heads' scales swapped
+
+
+def test_int8_vtoken_ones_and_constant_power_of_two(oracle_lib):
+    """v_token = 1 is the per-tensor path with v_scale 1; v_token = 2^-3 is
+    v_scale = 2^-3 (both products exact)."""
+    rng = np.random.default_rng(62)
+    qi = rng.integers(-127, 128, (1, 2, 30, 128), dtype=np.int8)
+    ki = rng.integers(-127, 128, (1, 1, 90, 128), dtype=np.int8)
+    vi = rng.integers(-127, 128, (1, 1, 90, 128), dtype=np.int8)
+    ones = np.ones((1, 1, 90), np.float32)
+    base = oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, window=40)
+    np.testing.assert_array_equal(oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, window=40, v_token=ones),
+                                  base)
+    np.testing.assert_array_equal(
+        oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, window=40, v_token=ones * 0.125),
+        oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 0.125, window=40))
+
+
+def test_int8_vtoken_close_to_fp_attention(oracle_lib):
+    """Per-token V quantisation approximates fp attention to the reference
+    gate's bar (rel_rms < 5e-2)."""
+    q, k, v = _int8_inputs(63, 1, 4, 2, 150, 300, 128)
+    qi, qs = oracle_lib.quant_pertoken(q)
+    ki, ks = oracle_lib.quant_pertoken(k)
+    vi, vt = oracle_lib.quant_pertoken(v)
+    out = oracle_lib.attention_int8(qi, ki, vi, qs, ks, 1.0, causal=True, v_token=vt)
+    ref = oracle_lib.attention(q, k, v, causal=True)
+    rel = np.sqrt(((out - ref) ** 2).mean() / (ref ** 2).mean())
+    assert rel < 5e-2
+
+
 # --------------------------------------------------------------------------- #
 # quantisers vs the torch calls the reference makes (rdnattention/__init__.py)
 # --------------------------------------------------------------------------- #
