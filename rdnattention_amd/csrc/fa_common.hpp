@@ -317,16 +317,6 @@ __device__ __forceinline__ void dma_load16_nt(i32x4_t rsrc, uint32_t voff, uint3
                  : "memory", "m0");
 }
 
-// Bytes of a strided row range [row0, n_rows) of a row-major tensor with
-// `row_bytes` per row and `stride_bytes` between rows, clamped to 32 bits.
-__device__ __forceinline__ uint32_t range_bytes(int64_t rows_left, int64_t stride_bytes, int64_t row_bytes) {
-    if (rows_left <= 0) {
-        return 0;
-    }
-    int64_t n = (rows_left - 1) * stride_bytes + row_bytes;
-    return n > 0xffffffffll ? 0xffffffffu : (uint32_t)n;
-}
-
 // Bytes of one key tile: min(rows_left, TILE_ROWS) rows of row_bytes at a
 // stride of stride_bytes (<= 2^25 and TILE_ROWS <= 64, so the result fits 32
 // bits), 0 when rows_left <= 0.

@@ -238,9 +238,19 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
     auto issue_tile = [&](int t, int slot) {
         const int kt0 = t * kWideBN;
         const int sk_left = p.mask.sk - kt0;
-        const i32x4_t rk = make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, range_bytes(sk_left, p.k_ss * 2, D * 2));
-        const i32x4_t rv =
-            make_rsrc_v(vbase + (int64_t)kt0 * p.v_ss + dv0, range_bytes(sk_left, p.v_ss * 2, C::DV * 2));
+        // one tile's byte range per descriptor (tile_bytes); the descriptor
+        // words are wave-uniform (one head per wave), and readfirstlane lets
+        // the compiler keep them in the SGPRs the DMA instruction needs
+        auto uniform = [](i32x4_t r) {
+            for (int e = 0; e < 4; e++) {
+                r[e] = __builtin_amdgcn_readfirstlane(r[e]);
+            }
+            return r;
+        };
+        const i32x4_t rk =
+            uniform(make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kWideBN>(sk_left, k_row_b, D * 2)));
+        const i32x4_t rv = uniform(
+            make_rsrc_v(vbase + (int64_t)kt0 * p.v_ss + dv0, tile_bytes<kWideBN>(sk_left, v_row_b, C::DV * 2)));
         const uint32_t sk = lds0 + slot * C::BUF_BYTES;
         const uint32_t sv = sk + C::TILE_K_BYTES;
         if (lane < C::KCH) {
