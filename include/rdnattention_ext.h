@@ -64,7 +64,7 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
 
 /* rdna_attention_forward_int8qk() with a per-token V scale: V row j of each
  * (batch, kv head) is dequantised by v_token_vec[b, kv_head, j] while the
- * kernel stages it, v'_j = fp16(v_i8[j] * v_token_vec[...]), and the
+ * kernel stages it, v'_j = fp16(v_i8[j] * fp16(v_token_vec[...])), and the
  * quantised P (the reference's pq = min(127, round(127 p))) multiplies these
  * fp16 rows: output = sum_j pq_j v'_j * v_scale / (127 l).  v_token_vec is a
  * contiguous fp32 [batch, num_kv_heads, key_seq_len] device array (4-byte

@@ -203,7 +203,7 @@ def attention_int8(qi, ki, vi, q_scale, k_scale, v_scale, causal=False, window=-
                    nthreads=None, v_token=None):
     """Kernel-exact INT8 emulation.  q_scale / k_scale: float or per-token array.
     v_token: per-token V scales [B, Hkv, Sk] (the library's extension; V row j
-    becomes fp16(fp32(v_j) * v_token_j) before P V), or None."""
+    becomes fp16(v_j * fp16(v_token_j)) before P V), or None."""
     qi = _c(qi, np.int8)
     ki = _c(ki, np.int8)
     vi = _c(vi, np.int8)

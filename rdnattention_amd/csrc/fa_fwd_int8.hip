@@ -110,16 +110,14 @@ __device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
     }
 }
 
-// 16 signed bytes of one V row -> two h8 of fp16(v * vs), the product rounded
-// once from fp32
-__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, float vs, h8& lo, h8& hi) {
-    const i8x8 a = __builtin_bit_cast(i8x8, i2{w[0], w[1]});
-    const i8x8 b = __builtin_bit_cast(i8x8, i2{w[2], w[3]});
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        lo[e] = (_Float16)((float)a[e] * vs);
-        hi[e] = (_Float16)((float)b[e] * vs);
-    }
+// 16 signed bytes of one V row -> two h8 of fp16(v * vs16), vs16 = fp16(vs):
+// the exact int8 -> fp16 conversion, then packed fp16 multiplies, each
+// product rounded once
+__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, _Float16 vs16, h8& lo, h8& hi) {
+    i8x16_to_h8x2(w, lo, hi);
+    const h8 s = {vs16, vs16, vs16, vs16, vs16, vs16, vs16, vs16};
+    lo *= s;
+    hi *= s;
 }
 
 // Scheme (the reference's, fa2_forward_int8qk.hip:281-382), per 64-key block b
@@ -135,8 +133,9 @@ __device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, float vs, h8& lo, h8&
 // no per-block int32 -> fp32 conversion.
 //
 // VTOK (an extension; the reference has no per-token V scale): V row j is
-// dequantised by its own scale vs_j while it is staged, v'_j = fp16(v_j * vs_j),
-// and P V runs on these fp16 values: O = O * corr + sum_j pq_j v'_j.
+// dequantised by its own scale vs_j while it is staged,
+// v'_j = fp16(v_j * fp16(vs_j)), and P V runs on these fp16 values:
+// O = O * corr + sum_j pq_j v'_j.
 template <int D, bool VTOK>
 __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     using C = I8Cfg<D>;
@@ -278,7 +277,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     if (x >= 1 && x <= n) {
                         h8 lo, hi;
                         if constexpr (VTOK) {
-                            i8x16_to_h8x2_scaled(vreg[it], vsreg[it], lo, hi);
+                            i8x16_to_h8x2_scaled(vreg[it], (_Float16)vsreg[it], lo, hi);
                         } else {
                             i8x16_to_h8x2(vreg[it], lo, hi);
                         }
