@@ -284,3 +284,23 @@ def test_pertoken_rope_cpu_path_matches_oracle():
         assert np.array_equal(xi.numpy(), ri) and np.allclose(xs.numpy(), rs, rtol=1e-6, atol=0)
     with pytest.raises(ValueError, match="both"):
         ra.quantize_int8_qk_pertoken(q, k, rot_cos=torch.from_numpy(cos))
+
+
+def test_pertoken_v_cpu_path_matches_oracle():
+    """quantize_int8_pertoken_v on a CPU tensor: the per-token formula of
+    quantize_int8_qk_pertoken (rdnattention/__init__.py:335-339), as the
+    oracle's quantiser computes it."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import rdnattention_amd as ra
+
+    g = torch.Generator().manual_seed(18)
+    v = torch.randn(2, 3, 50, 64, generator=g).half()
+    v[0, 0, 3] = 0  # an all-zero row: scale 1
+    vi, vt = ra.quantize_int8_pertoken_v(v)
+    ri, rs = oracle.quant_pertoken(v.float().numpy())
+    assert vi.dtype == torch.int8 and vt.shape == (2, 3, 50) and vt.is_contiguous()
+    assert np.array_equal(vi.numpy(), ri) and np.allclose(vt.numpy(), rs, rtol=1e-6, atol=0)
+    assert vt[0, 0, 3].item() == 1.0
