@@ -4,6 +4,7 @@
                     [--no-cpu] [--no-secondary]
     python bench.py --copy-calibration          (a plain copy of known size)
     python bench.py --pmc-summary DIR           (rocprofv3 counter CSVs -> table)
+    python bench.py --gemm-ceiling 8192         (fp16 torch.matmul: the MFMA ceiling)
 
 Default workload (the headline metric): FP16 causal GQA prefill with
 in-kernel RoPE (theta 10000), B=4, Hq=32, Hkv=8, S=key_S=4096, D=128,
@@ -25,6 +26,8 @@ Prints ONE JSON line:
   cpu_baseline  the CPU oracle (C, fp64, threaded) on a bounded sample of
              the same workload on the host cores ("port");
   cpu_sdpa   torch's CPU scaled_dot_product_attention on a bounded sample;
+  parity_vs_oracle  the measured step's output on the CPU baseline's sample
+             against the oracle's output there (max/mean abs, rel_rms);
   secondary  the other measured shapes: INT8 vs FP16 on the INT8 shape,
              split-K decode HBM bandwidth, large-head sliding windows.
 """
@@ -197,7 +200,7 @@ def make_step(wl: Workload, dev, host=None):
     workload's seed) and a closure running one forward."""
     import torch
 
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     g = torch.Generator(device=dev).manual_seed(wl.seed)
 
@@ -218,8 +221,13 @@ def make_step(wl: Workload, dev, host=None):
         cos = cos.to(dev) if cos is not None else None
         sin = sin.to(dev) if sin is not None else None
         out = torch.empty_like(q)
-        return lambda: ra.attention_forward_into(q, k, v, out, is_causal=wl.causal, window_size=wl.window,
-                                                 rot_cos=cos, rot_sin=sin)
+
+        def step():
+            ra.attention_forward_into(q, k, v, out, is_causal=wl.causal, window_size=wl.window, rot_cos=cos,
+                                      rot_sin=sin)
+
+        step.out = out
+        return step
     if wl.kind == "int8":
         qf = randn(wl.b, wl.hq, wl.sq, wl.d)
         kf = randn(wl.b, wl.hkv, wl.sk, wl.d)
@@ -256,7 +264,7 @@ def int8_quantized_e2e(dev, steps: int = 10, warmup: int = 20):
     the output by v_channel)."""
     import torch
 
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     g = torch.Generator(device=dev).manual_seed(7)
     b, hq, hkv, s, d = 2, 32, 8, 8192, 128
@@ -313,7 +321,7 @@ def time_steps(step, steps: int, warmup: int):
     kernel launches, wall s of the timed steps)."""
     import torch
 
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     for _ in range(warmup):
         step()
@@ -390,18 +398,35 @@ def cpu_oracle_baseline(wl: Workload, host, budget_s: float = 12.0):
         if wl.rope:
             qs = oracle.rope(qs, cn, sn)
             ks = oracle.rope(ks, cn, sn)
-        oracle.attention(qs, ks, vs, causal=wl.causal, window=wl.window, nthreads=threads)
-        return time.perf_counter() - t0
+        o = oracle.attention(qs, ks, vs, causal=wl.causal, window=wl.window, nthreads=threads)
+        return time.perf_counter() - t0, o
 
-    t1 = run(1)
+    t1, _ = run(1)
     n = max(1, min(units, int(budget_s / max(t1, 1e-6))))
-    t = run(n)
+    t, ref = run(n)
     flops = attn_flops(1, n * ratio, wl.sq, wl.sk, wl.d, wl.causal, wl.window)
     return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": (f"CPU oracle (C, fp64 accumulation, {threads} threads) on {cpu_model()} "
                        f"(os.cpu_count()={os.cpu_count()}): {n} of {units} (batch, kv head) units = "
                        f"{n * ratio} of {wl.b * wl.hq} query-head rows of S={wl.sq}, RoPE included, "
-                       f"one run of {t:.2f} s")}
+                       f"one run of {t:.2f} s")}, ref
+
+
+def sample_parity(wl: Workload, gpu_out, ref):
+    """The GPU output of the measured step against the oracle's output for the
+    CPU baseline's sample (its first query heads in batch-major order): max
+    and mean absolute error and rel_rms, with the FP16 bars they must meet."""
+    import numpy as np
+
+    rows = ref.shape[1]
+    got = gpu_out.reshape(1, wl.b * wl.hq, wl.sq, wl.d)[:, :rows].float().cpu().numpy().astype(np.float64)
+    d = np.abs(got - ref)
+    rr = float(np.sqrt((ref.astype(np.float64) ** 2).mean()))
+    res = {"max_abs": float(d.max()), "mean_abs": float(d.mean()),
+           "rel_rms": float(np.sqrt((d ** 2).mean()) / rr) if rr > 0 else float(np.sqrt((d ** 2).mean())),
+           "query_head_rows": f"{rows} of {wl.b * wl.hq}", "bar": {"max_abs": 2e-3, "mean_abs": 2e-4}}
+    res["ok"] = bool(np.isfinite(got).all() and res["max_abs"] <= 2e-3 and res["mean_abs"] <= 2e-4)
+    return res
 
 
 def cpu_sdpa_baseline(wl: Workload, host, budget_s: float = 12.0):
@@ -475,6 +500,34 @@ def copy_calibration(steps: int = 5) -> int:
     return 0
 
 
+def gemm_ceiling(n: int = 8192, steps: int = 20, warmup: int = 50) -> int:
+    """The practical fp16 MFMA ceiling of this GPU: torch.matmul (hipBLASLt)
+    of two n x n fp16 matrices, timed with HIP events after `warmup` untimed
+    products (the clock ramp), 2 n^3 FLOPs each.  Run it under rocprofv3
+    --pmc SQ_VALU_MFMA_BUSY_CYCLES ... for the library GEMM's MFMA-busy share."""
+    import torch
+
+    g = torch.Generator(device="cuda:0").manual_seed(0)
+    a = torch.randn(n, n, device="cuda:0", generator=g).half()
+    b = torch.randn(n, n, device="cuda:0", generator=g).half()
+    for _ in range(warmup):
+        c = torch.matmul(a, b)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        c = torch.matmul(a, b)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    tflops = 2 * n ** 3 / (ms * 1e-3) / 1e12
+    print(json.dumps({"gemm": f"fp16 {n}x{n}x{n} torch.matmul", "ms": round(ms, 4), "tflops": round(tflops, 1),
+                      "frac_of_dense_peak": round(tflops / FP16_PEAK_TFLOPS, 4), "checksum": float(c[0, 0])}),
+          flush=True)
+    return 0
+
+
 def pmc_summary(directory: str) -> int:
     """Mean per-dispatch counter values per kernel from rocprofv3's
     *counter_collection.csv files under `directory`."""
@@ -506,6 +559,8 @@ def main(argv=None):
     ap.add_argument("--no-secondary", action="store_true", help="measure the selected workload only")
     ap.add_argument("--copy-calibration", action="store_true", help="run the 1 GiB copy used to scale counters")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 counter CSVs under DIR")
+    ap.add_argument("--gemm-ceiling", type=int, metavar="N", default=0,
+                    help="time an N^3 fp16 torch.matmul (the practical MFMA ceiling) and exit")
     args = ap.parse_args(argv)
     if args.pmc_summary:
         return pmc_summary(args.pmc_summary)
@@ -515,10 +570,12 @@ def main(argv=None):
         return 2
     if args.copy_calibration:
         return copy_calibration()
+    if args.gemm_ceiling:
+        return gemm_ceiling(args.gemm_ceiling)
 
     import torch
 
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     dev = torch.device("cuda:0")
     name = args.workload
@@ -526,7 +583,6 @@ def main(argv=None):
     host = cpu_inputs(wl) if wl.kind == "f16" else None
     step = make_step(wl, dev, host)
     ms_step, kernel_ms, launches, wall = time_steps(step, args.steps, args.warmup)
-    del step
     if launches != args.steps:
         raise RuntimeError(f"kernel timer saw {launches} launches for {args.steps} steps")
     if wl.kind == "decode":
@@ -560,9 +616,11 @@ def main(argv=None):
             secondary["int8_quantized_end_to_end"] = {"error": str(e)}
         torch.cuda.empty_cache()
 
-    cpu = sdpa = None
+    cpu = sdpa = parity = None
     if not args.no_cpu and host is not None:
-        cpu = cpu_oracle_baseline(wl, host)
+        cpu, ref = cpu_oracle_baseline(wl, host)
+        parity = sample_parity(wl, step.out, ref)
+        del ref
         sdpa = cpu_sdpa_baseline(wl, host)
 
     line = {
@@ -584,6 +642,7 @@ def main(argv=None):
         "roofline": roofline(wl, kernel_ms, profiled_traffic(name, wl)),
         "cpu_baseline": cpu,
         "cpu_sdpa": sdpa,
+        "parity_vs_oracle": parity,
         "kernel": wl.kernel,
         "kernel_ms_mean": round(kernel_ms, 4),
         "algorithmic_bytes_per_launch": wl.io_bytes,

@@ -2,7 +2,7 @@
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
 import this package, and only to check results against.  The shipped library
-(``rdnattention_amd``) never imports it and has no CPU fallback.
+(``rdnattention``) never imports it and has no CPU fallback.
 
 This module is a thin numpy/ctypes layer over ``attn_oracle.c`` (built by
 ``oracle/Makefile`` into ``oracle/liboracle.so``).  The C file restates the

@@ -1,4 +1,4 @@
-"""rdnattention_amd -- FlashAttention-2 forward for MI355X (gfx950), drop-in
+"""rdnattention -- FlashAttention-2 forward for MI355X (gfx950), a drop-in
 for the ``rdnattention`` Python package of dmonkman/RDNAttention.
 
 The public surface is the reference's (rdnattention/__init__.py:360-363):
@@ -11,7 +11,7 @@ checks and exception types.  Every call goes through ``librdnattention.so``
 fallback: a missing library raises ``RDNAttentionError``.
 
     >>> import torch
-    >>> from rdnattention_amd import flash_attn
+    >>> from rdnattention import flash_attn
     >>> q = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
     >>> k = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
     >>> v = torch.randn(1, 8, 512, 64, dtype=torch.float16, device="cuda")
@@ -43,8 +43,22 @@ class RDNAttentionError(Exception):
     """Raised for any rdnattention library error."""
 
 
+def _library_candidates() -> list:
+    """Search order after RDNATTENTION_LIB (rdnattention/__init__.py:54-61): the
+    development build build/librdnattention.so and the packaged
+    lib/librdnattention.so, the development build first in a source checkout
+    (where the native sources rdnattention_amd/csrc sit next to the package),
+    so that a stale lib/ never shadows a rebuild."""
+    here = Path(__file__).resolve().parent
+    packaged = here / "lib" / "librdnattention.so"
+    dev = here.parent / "build" / "librdnattention.so"
+    in_source_tree = (here.parent / "rdnattention_amd" / "csrc").is_dir()
+    return [dev, packaged] if in_source_tree else [packaged, dev]
+
+
 def _find_library() -> Path:
-    """RDNATTENTION_LIB, else the in-tree build (rdnattention/__init__.py:37-73)."""
+    """RDNATTENTION_LIB, else the candidates of _library_candidates()
+    (rdnattention/__init__.py:37-73; Linux only: this build targets ROCm)."""
     if platform.system() != "Linux":
         raise RDNAttentionError(f"Unsupported platform: {platform.system()} (this build targets Linux/ROCm)")
     override = os.environ.get("RDNATTENTION_LIB")
@@ -54,12 +68,19 @@ def _find_library() -> Path:
             raise RDNAttentionError(f"RDNATTENTION_LIB points at a missing file: {path}")
         logger.debug("Loading library from RDNATTENTION_LIB=%s", path)
         return path
-    path = Path(__file__).resolve().parent / "lib" / "librdnattention.so"
-    if path.exists():
-        return path
+    candidates = _library_candidates()
+    for path in candidates:
+        if path.exists():
+            others = [c for c in candidates if c != path and c.exists()]
+            if others and path == candidates[0] and path.parent.name == "build":
+                logger.warning("Ignoring the packaged %s: this is a source checkout, so %s takes priority. "
+                               "Delete lib/ to silence this.", others[0], path)
+            logger.debug("Loading library from %s", path)
+            return path
     raise RDNAttentionError(
-        f"Could not find the rdnattention library ({path}). Build it first: "
-        "python -m rdnattention_amd._build")
+        "Could not find the rdnattention library (librdnattention.so). Build it first "
+        "(python -m rdnattention._build), or install the wheel.\n"
+        f"Searched: {[str(p) for p in candidates]}")
 
 
 _VP = ctypes.c_void_p
@@ -134,8 +155,21 @@ def _validate_inputs(query, key, value, expected_dtype) -> None:
             raise ValueError(f"{name} must be 4D [batch, heads, seq, head_dim], got shape {tuple(t.shape)}")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous - call .contiguous() first")
+    _check_shapes(query, key, value)
+
+
+def _check_shapes(query, key, value) -> None:
+    """The shape relations every kernel relies on: one batch size, V shaped
+    like K, one head_dim, and a whole number of query heads per kv head.  The
+    first and last are the reference's checks (rdnattention/__init__.py:151-
+    155); the kernels would read past the end of a smaller K/V otherwise, so
+    the middle two are added here."""
     if query.shape[0] != key.shape[0] or query.shape[0] != value.shape[0]:
         raise ValueError(f"Batch size must match: Q={query.shape}, K={key.shape}, V={value.shape}")
+    if tuple(key.shape) != tuple(value.shape):
+        raise ValueError(f"key and value must have the same shape: K={tuple(key.shape)}, V={tuple(value.shape)}")
+    if key.shape[3] != query.shape[3]:
+        raise ValueError(f"key head_dim ({key.shape[3]}) must equal query head_dim ({query.shape[3]})")
     if key.shape[1] == 0 or query.shape[1] % key.shape[1] != 0:
         raise ValueError(f"Q heads ({query.shape[1]}) must be a multiple of K heads ({key.shape[1]})")
 
@@ -238,6 +272,7 @@ def attention_forward_into(query, key, value, output, *, is_causal: bool = False
             raise ValueError(f"{name} must have a contiguous head_dim axis")
     if output.shape != query.shape:
         raise ValueError("output must have the shape of query")
+    _check_shapes(query, key, value)
     batch, heads, seq_len, head_dim = query.shape
     _, kv_heads, key_seq_len, _ = key.shape
     cos_ptr, sin_ptr, has_rope = _rope_ptrs(rot_cos, rot_sin, query, seq_len, key_seq_len, head_dim)
@@ -324,6 +359,7 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
             raise ValueError(f"{name} must be a 4D int8 HIP tensor")
     if output.dtype != torch.float16 or output.shape != query.shape or not output.is_cuda:
         raise ValueError("output must be a float16 HIP tensor with the shape of query")
+    _check_shapes(query, key, value)
     batch, heads, seq_len, head_dim = query.shape
     _, kv_heads, key_seq_len, _ = key.shape
 
@@ -553,12 +589,11 @@ def flash_attn_int8qk_quantized(query, key, value, is_causal: bool = False, wind
             raise ValueError(f"{name} must be on a HIP device")
         if t.dim() != 4:
             raise ValueError(f"{name} must be 4D [batch, heads, seq, head_dim], got shape {tuple(t.shape)}")
-    if query.shape[0] != key.shape[0] or query.shape[0] != value.shape[0]:
-        raise ValueError(f"Batch size must match: Q={query.shape}, K={key.shape}, V={value.shape}")
     heads, kv_heads = query.shape[1], key.shape[1]
     if kv_heads == 0 or heads % kv_heads != 0:
         raise RDNAttentionError(
             f"flash_attn_int8qk: query heads ({heads}) must be a positive multiple of key/value heads ({kv_heads})")
+    _check_shapes(query, key, value)
     _check_head_dim(query.shape[-1], "flash_attn_int8qk", allowed=SUPPORTED_HEAD_DIMS_INT8)
     if not has_device():
         raise RDNAttentionError("no usable HIP device found")

@@ -1,13 +1,15 @@
 """Builds librdnattention.so for gfx950 with hipcc (no cmake, no JIT cache).
 
-    python -m rdnattention_amd._build [--arch gfx950] [--no-int8] [-v]
+    python -m rdnattention._build [--arch gfx950] [--no-int8] [--out DIR] [-v]
 
-Objects go to rdnattention_amd/_build/, the library to
-rdnattention_amd/lib/librdnattention.so (in-tree, so it travels with the
-repository snapshot to the GPU machine), and the compiler's per-kernel
-resource usage to rdnattention_amd/lib/kernel_resources.json.  Mirrors the reference's build
-options (CMakeLists.txt:3-5 forced Release, :33 RDNATTENTION_ENABLE_INT8)
-for one architecture, gfx950.
+Sources are rdnattention_amd/csrc/*.{hip,cpp}.  Objects go to build/obj/,
+the library to build/librdnattention.so -- the development build that the
+package prefers in a source checkout, as the reference's wrapper prefers its
+CMake build/ directory (rdnattention/__init__.py:55-61) -- and the
+compiler's per-kernel resource usage to build/kernel_resources.json.  The
+wheel (setup.py) copies the library into rdnattention/lib/.  Mirrors the
+reference's build options (CMakeLists.txt:3-5 forced Release, :33
+RDNATTENTION_ENABLE_INT8) for one architecture, gfx950.
 """
 from __future__ import annotations
 
@@ -23,13 +25,13 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-CSRC = PKG / "csrc"
-OBJ = PKG / "_build"
-LIB_DIR = PKG / "lib"
-LIB = LIB_DIR / "librdnattention.so"
+CSRC = ROOT / "rdnattention_amd" / "csrc"
+BUILD = ROOT / "build"
+LIB_NAME = "librdnattention.so"
+LIB = BUILD / LIB_NAME
 # per-kernel resource usage of the last build (VGPRs, AGPRs, scratch, LDS,
 # occupancy), from the compiler's kernel-resource-usage remarks
-RESOURCES = LIB_DIR / "kernel_resources.json"
+RESOURCES = BUILD / "kernel_resources.json"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in device code (the host pass
@@ -60,8 +62,8 @@ def parse_resource_remarks(text: str, source: str):
     return kernels
 
 
-def _compile(src: Path, arch: str, defines, verbose: bool):
-    out = OBJ / (src.name + ".o")
+def _compile(src: Path, obj_dir: Path, arch: str, defines, verbose: bool):
+    out = obj_dir / (src.name + ".o")
     if src.suffix == ".hip":
         cmd = [HIPCC, "-x", "hip", f"--offload-arch={arch}", *COMMON, *DEVICE_FLAGS, *defines,
                "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(out)]
@@ -80,34 +82,41 @@ def _compile(src: Path, arch: str, defines, verbose: bool):
     return out, parse_resource_remarks(r.stderr, src.name)
 
 
-def build(arch: str = "gfx950", int8: bool = True, verbose: bool = False, jobs: int | None = None) -> Path:
-    OBJ.mkdir(exist_ok=True)
-    LIB_DIR.mkdir(exist_ok=True)
+def build(arch: str = "gfx950", int8: bool = True, verbose: bool = False, jobs: int | None = None,
+          out_dir: Path | None = None) -> Path:
+    """Compile and link; returns the library path (out_dir/librdnattention.so,
+    default build/).  int8=False is the reference's RDNATTENTION_ENABLE_INT8=OFF
+    build: the INT8 entry points stay exported and return -4."""
+    out_dir = Path(out_dir) if out_dir is not None else BUILD
+    obj_dir = out_dir / ("obj" if int8 else "obj_noint8")
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    lib = out_dir / LIB_NAME
     defines = [] if int8 else ["-DRDNATTENTION_NO_INT8"]
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        results = list(ex.map(lambda s: _compile(s, arch, defines, verbose), srcs))
+        results = list(ex.map(lambda s: _compile(s, obj_dir, arch, defines, verbose), srcs))
     objs = [o for o, _ in results]
-    RESOURCES.write_text(json.dumps([k for _, ks in results for k in ks], indent=1))
-    tmp = LIB.with_suffix(".so.tmp")
+    (out_dir / RESOURCES.name).write_text(json.dumps([k for _, ks in results for k in ks], indent=1))
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={arch}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    shutil.move(str(tmp), str(LIB))
-    return LIB
+    shutil.move(str(tmp), str(lib))
+    return lib
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--arch", default="gfx950")
     ap.add_argument("--no-int8", action="store_true")
+    ap.add_argument("--out", type=Path, default=None, help="output directory (default: build/)")
     ap.add_argument("-v", "--verbose", action="store_true")
     args = ap.parse_args(argv)
-    path = build(args.arch, not args.no_int8, args.verbose)
+    path = build(args.arch, not args.no_int8, args.verbose, out_dir=args.out)
     print(path)
 
 

@@ -44,6 +44,11 @@ bool stride_ok(const int64_t s[3], int64_t mult) {
 
 constexpr uint32_t kMaxSeq = 1u << 30;
 
+#if defined(RDNATTENTION_NO_INT8)
+// the reference's FP16-only build text (src/c_api.cpp:151-153)
+constexpr const char* kNoInt8 = "this library was built without the INT8 kernel - use rdna_attention_forward() instead";
+#endif
+
 // Shared checks.  Returns "" when the arguments are acceptable.
 std::string check_common(const AttnArgs& a, uint32_t B, uint32_t Hq, uint32_t Hkv, uint32_t Sq, uint32_t Sk,
                          int64_t in_mult) {
@@ -258,8 +263,7 @@ RDNA_API int32_t rdna_attention_forward_int8qk(const void* q, const void* k, con
     (void)o_stride_b, (void)o_stride_h, (void)o_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads;
     (void)seq_len, (void)key_seq_len, (void)head_dim, (void)scale, (void)q_scale, (void)k_scale, (void)v_scale;
     (void)q_scale_vec, (void)k_scale_vec, (void)causal, (void)window_size, (void)hip_stream;
-    set_error("Attention (int8qk) unavailable: %s",
-              "this library was built without the INT8 kernel - use rdna_attention_forward() instead");
+    set_error("Attention (int8qk) unavailable: %s", kNoInt8);
     return -4;
 #else
     std::string err;
@@ -288,8 +292,7 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
     (void)o_stride_b, (void)o_stride_h, (void)o_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads;
     (void)seq_len, (void)key_seq_len, (void)head_dim, (void)scale, (void)q_scale, (void)k_scale, (void)v_scale;
     (void)q_scale_vec, (void)k_scale_vec, (void)v_channel_vec, (void)causal, (void)window_size, (void)hip_stream;
-    set_error("Attention (int8qk) unavailable: %s",
-              "this library was built without the INT8 kernel - use rdna_attention_forward() instead");
+    set_error("Attention (int8qk) unavailable: %s", kNoInt8);
     return -4;
 #else
     std::string err;
@@ -319,8 +322,7 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vtoken(
     (void)o_stride_b, (void)o_stride_h, (void)o_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads;
     (void)seq_len, (void)key_seq_len, (void)head_dim, (void)scale, (void)q_scale, (void)k_scale, (void)v_scale;
     (void)q_scale_vec, (void)k_scale_vec, (void)v_token_vec, (void)causal, (void)window_size, (void)hip_stream;
-    set_error("Attention (int8qk) unavailable: %s",
-              "this library was built without the INT8 kernel - use rdna_attention_forward() instead");
+    set_error("Attention (int8qk) unavailable: %s", kNoInt8);
     return -4;
 #else
     if (v_token_vec == nullptr) {
@@ -394,6 +396,13 @@ RDNA_API int32_t rdna_int8_qk_scores(const void* q, const void* k, int32_t* scor
                                      int64_t k_stride_s, uint32_t batch_size, uint32_t num_heads,
                                      uint32_t num_kv_heads, uint32_t seq_len, uint32_t key_seq_len,
                                      uint32_t head_dim, void* hip_stream) {
+#if defined(RDNATTENTION_NO_INT8)
+    (void)q, (void)k, (void)scores, (void)q_stride_b, (void)q_stride_h, (void)q_stride_s, (void)k_stride_b;
+    (void)k_stride_h, (void)k_stride_s, (void)batch_size, (void)num_heads, (void)num_kv_heads, (void)seq_len;
+    (void)key_seq_len, (void)head_dim, (void)hip_stream;
+    set_error("Attention (int8qk) unavailable: %s", kNoInt8);
+    return -4;
+#else
     std::string err;
     AttnArgs a;
     a.q = q;
@@ -426,6 +435,7 @@ RDNA_API int32_t rdna_int8_qk_scores(const void* q, const void* k, int32_t* scor
     }
     set_error("Attention (int8qk) failed: %s", err);
     return -3;
+#endif
 }
 
 // ---------------------------------------------------------------------------

@@ -40,6 +40,8 @@
 
 namespace rdna_amd {
 
+#if !defined(RDNATTENTION_NO_INT8)
+
 float softmax_log2_scale(float scale);
 
 namespace {
@@ -632,5 +634,19 @@ int int8_scores(const AttnArgs& a, int32_t* scores, hipStream_t stream, std::str
     }
     return 0;
 }
+
+#else // RDNATTENTION_NO_INT8: the reference's RDNATTENTION_ENABLE_INT8=OFF build (CMakeLists.txt:33)
+
+int fwd_int8(const AttnArgs&, hipStream_t, std::string& err) {
+    err = "this library was built without the INT8 kernel";
+    return -1;
+}
+
+int int8_scores(const AttnArgs&, int32_t*, hipStream_t, std::string& err) {
+    err = "this library was built without the INT8 kernel";
+    return -1;
+}
+
+#endif
 
 } // namespace rdna_amd

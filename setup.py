@@ -1,15 +1,19 @@
-"""Wheel build: compiles librdnattention.so for gfx950 with hipcc into
-rdnattention_amd/lib (rdnattention_amd/_build.py) before packaging it, so a
-wheel always carries the library built from its own sources.
+"""Wheel build: compiles librdnattention.so for gfx950 with hipcc
+(rdnattention/_build.py) and places it in rdnattention/lib, the reference
+wheel's layout (pyproject.toml:6, :66-67), so a wheel always carries the
+library built from its own sources.
 
     pip wheel . --no-deps --no-build-isolation
 """
 import importlib.util
+import shutil
 from pathlib import Path
 
 from setuptools import setup
 from setuptools.command.build_py import build_py
 from setuptools.dist import Distribution
+
+ROOT = Path(__file__).resolve().parent
 
 
 class BinaryDistribution(Distribution):
@@ -22,28 +26,28 @@ class BuildWithLibrary(build_py):
     def run(self):
         # load the build module by path: importing the package is not needed
         # (and would import the runtime wrapper) to compile the library
-        path = Path(__file__).resolve().parent / "rdnattention_amd" / "_build.py"
-        spec = importlib.util.spec_from_file_location("rdnattention_amd_build", path)
+        spec = importlib.util.spec_from_file_location("rdnattention_build", ROOT / "rdnattention" / "_build.py")
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)
-        mod.build()
+        lib = mod.build()
+        dest = ROOT / "rdnattention" / "lib"
+        dest.mkdir(exist_ok=True)
+        shutil.copy2(lib, dest / lib.name)
         super().run()
 
 
 setup(
-    name="rdnattention-amd",
+    name="rdnattention",
     version="0.1.0",
     description="FlashAttention-2 forward for AMD MI355X (gfx950): a drop-in for RDNAttention's attention path",
-    long_description=(Path(__file__).resolve().parent / "README.md").read_text(),
+    long_description=(ROOT / "README.md").read_text(),
     long_description_content_type="text/markdown",
     python_requires=">=3.9",
     # the wrapper takes torch (ROCm) tensors; torch is not pinned, as in the
     # reference (pyproject.toml:39-49)
-    install_requires=["numpy"],
-    packages=["rdnattention_amd"],
-    # the library sits in the package's lib/ directory, as in the reference's
-    # wheel (rdnattention/lib, pyproject.toml:66-67)
-    package_data={"rdnattention_amd": ["lib/librdnattention.so", "csrc/*.hip", "csrc/*.hpp", "csrc/*.cpp"]},
+    install_requires=[],
+    packages=["rdnattention"],
+    package_data={"rdnattention": ["lib/librdnattention.so"]},
     cmdclass={"build_py": BuildWithLibrary},
     distclass=BinaryDistribution,
 )

@@ -25,9 +25,9 @@ def log(msg: str) -> None:
 
 
 def lib():
-    import rdnattention_amd
+    import rdnattention
 
-    return rdnattention_amd._lib_handle()
+    return rdnattention._lib_handle()
 
 
 def stream_ptr():

@@ -16,18 +16,18 @@ import numpy as np
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-LIB = ROOT / "rdnattention_amd" / "lib" / "librdnattention.so"
+LIB = ROOT / "build" / "librdnattention.so"
 
 
 @pytest.fixture(scope="module")
 def lib():
     if not LIB.exists():
-        from rdnattention_amd import _build
+        from rdnattention import _build
 
         _build.build()
-    import rdnattention_amd
+    import rdnattention
 
-    return rdnattention_amd._lib_handle()
+    return rdnattention._lib_handle()
 
 
 def _declared_symbols():
@@ -144,9 +144,9 @@ def test_int8_argument_errors(lib, kw, msg):
 def test_int8_vtoken_argument_errors(lib):
     """rdna_attention_forward_int8qk_vtoken: the scale array is required, 4-byte
     aligned, and checked before any HIP call."""
-    import rdnattention_amd
+    import rdnattention
 
-    rdnattention_amd._lib_handle()
+    rdnattention._lib_handle()
     hold, p = _buf()
     s = (8 * 8 * 64, 8 * 64, 64)
 
@@ -175,7 +175,7 @@ def test_has_device_without_gpu(lib):
 def test_python_type_errors():
     import torch
 
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     with pytest.raises(TypeError):
         ra.flash_attn(np.zeros((1, 1, 1, 64)), None, None)
@@ -185,7 +185,7 @@ def test_python_type_errors():
 
 
 def test_python_head_dim_lists():
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     assert ra.SUPPORTED_HEAD_DIMS == tuple(range(32, 513, 32))
     assert ra.SUPPORTED_HEAD_DIMS_INT8 == (64, 128)
@@ -198,7 +198,7 @@ def test_python_head_dim_lists():
 
 
 def test_python_missing_library(monkeypatch, tmp_path):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     monkeypatch.setenv("RDNATTENTION_LIB", str(tmp_path / "nope.so"))
     monkeypatch.setattr(ra, "_lib", None)
@@ -270,7 +270,7 @@ def test_pertoken_rope_cpu_path_matches_oracle():
     import torch
 
     import oracle
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     g = torch.Generator().manual_seed(17)
     q = torch.randn(1, 2, 40, 64, generator=g).half()
@@ -294,7 +294,7 @@ def test_pertoken_v_cpu_path_matches_oracle():
     import torch
 
     import oracle
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     g = torch.Generator().manual_seed(18)
     v = torch.randn(2, 3, 50, 64, generator=g).half()

@@ -37,10 +37,35 @@ def test_cpu_baselines_small(oracle_lib):
 
     wl = bench.Workload("f16", 1, 4, 2, 256, 256, 64, True, -1, True, 0, 1.0, "fa_fwd_f16_pp<64>")
     host = bench.cpu_inputs(wl)
-    r = bench.cpu_oracle_baseline(wl, host, budget_s=0.5)
+    r, ref = bench.cpu_oracle_baseline(wl, host, budget_s=0.5)
     assert r["value"] > 0 and r["cores"] >= 1 and r["kind"] == "port"
+    assert ref.shape[0] == 1 and ref.shape[1] % (wl.hq // wl.hkv) == 0 and ref.shape[2:] == (wl.sq, wl.d)
     r = bench.cpu_sdpa_baseline(wl, host, budget_s=0.5)
     assert r["value"] > 0 and r["cores"] >= 1
+
+
+def test_sample_parity(oracle_lib):
+    """sample_parity compares the sample's query heads (batch-major) of the
+    step's output with the oracle's: the oracle's own output passes, a planted
+    error in one element of the sample fails, and rows past the sample are not
+    read."""
+    import torch
+
+    import bench
+
+    wl = bench.Workload("f16", 2, 4, 2, 64, 64, 32, True, -1, False, 0, 1.0, "fa_fwd_f16_pp<32>")
+    q, k, v, _, _ = bench.cpu_inputs(wl)
+    full = oracle_lib.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=True)
+    ref = full.reshape(1, 8, 64, 32)[:, :6]
+    out = torch.from_numpy(full).half()
+    assert bench.sample_parity(wl, out, ref)["ok"]
+    bad = out.clone()
+    bad.view(1, 8, 64, 32)[0, 5, 17, 3] += 0.01
+    r = bench.sample_parity(wl, bad, ref)
+    assert not r["ok"] and abs(r["max_abs"] - 0.01) < 1e-3
+    past = out.clone()
+    past.view(1, 8, 64, 32)[0, 7] = 5.0
+    assert bench.sample_parity(wl, past, ref)["ok"]
 
 
 def test_io_bytes_and_flops():

@@ -28,9 +28,9 @@ _U32, _I32, _F32 = ctypes.c_uint32, ctypes.c_int32, ctypes.c_float
 def cxx():
     if not CALLER.exists():
         pytest.fail(f"{CALLER} is not built (run __graft_entry__.build())")
-    import rdnattention_amd
+    import rdnattention
 
-    rdnattention_amd._lib_handle()  # the same librdnattention.so the caller links
+    rdnattention._lib_handle()  # the same librdnattention.so the caller links
     c = ctypes.CDLL(str(CALLER))
     c.cxx_forward_f16.argtypes = [_VP] * 6 + [_I64P, _U32P, _F32, _U32, _U32, _I32, _VP, ctypes.c_char_p, _I32]
     c.cxx_forward_f16.restype = _I32

@@ -92,8 +92,8 @@ def test_splitk_unsupported_shape_is_rejected(gpu):
     q = torch.zeros(1, 8, 9, 128, dtype=torch.float16, device=gpu)  # ratio 4 x 9 rows = 36 columns > 32
     k = torch.zeros(1, 2, 100, 128, dtype=torch.float16, device=gpu)
     out = torch.empty_like(q)
-    import rdnattention_amd
+    import rdnattention
 
     assert forward_raw(q, k, k, out, path=PATH_SPLITK) == -3
-    assert "split-K" in rdnattention_amd.last_error()
+    assert "split-K" in rdnattention.last_error()
     assert forward_raw(q, k, k, out, path=0) == 0  # auto falls back to the prefill kernel

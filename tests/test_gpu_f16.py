@@ -107,8 +107,8 @@ HEAD_DIM_VARIANTS = [
 @pytest.mark.parametrize("d", list(range(32, 513, 32)))
 @pytest.mark.parametrize("variant", HEAD_DIM_VARIANTS, ids=[v[0] for v in HEAD_DIM_VARIANTS])
 def test_head_dim_python_path(gpu, oracle_lib, d, variant):
-    """tests/head_dim.py through rdnattention_amd.flash_attn (8 heads, N(0,1))."""
-    import rdnattention_amd
+    """tests/head_dim.py through rdnattention.flash_attn (8 heads, N(0,1))."""
+    import rdnattention
 
     name, kvdiv, s_len, ks_len, causal, window = variant
     torch.manual_seed(1234)
@@ -117,7 +117,7 @@ def test_head_dim_python_path(gpu, oracle_lib, d, variant):
     q = torch.randn(1, h, s_len, d, dtype=torch.float16)
     k = torch.randn(1, kvh, ks_len, d, dtype=torch.float16)
     v = torch.randn(1, kvh, ks_len, d, dtype=torch.float16)
-    out = rdnattention_amd.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal, window_size=window)
+    out = rdnattention.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal, window_size=window)
     torch.cuda.synchronize()
     ref = reference_f16(q, k, v, causal, window)
     assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_{name}")
@@ -136,8 +136,8 @@ ROPE_CASES = [
 
 @pytest.mark.parametrize("case", ROPE_CASES, ids=[c[0] for c in ROPE_CASES])
 def test_rope_cases(gpu, oracle_lib, case):
-    """tests/rope.py:66-96 through rdnattention_amd.flash_attn with in-kernel RoPE."""
-    import rdnattention_amd
+    """tests/rope.py:66-96 through rdnattention.flash_attn with in-kernel RoPE."""
+    import rdnattention
 
     name, b, h, kh, s, ks, d, causal = case
     torch.manual_seed(7)
@@ -145,7 +145,7 @@ def test_rope_cases(gpu, oracle_lib, case):
     k = torch.randn(b, kh, ks, d, dtype=torch.float16)
     v = torch.randn(b, kh, ks, d, dtype=torch.float16)
     cos, sin = oracle.rope_tables(max(s, ks), d)
-    out = rdnattention_amd.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal,
+    out = rdnattention.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=causal,
                                       rot_cos=torch.from_numpy(cos).to(gpu), rot_sin=torch.from_numpy(sin).to(gpu))
     torch.cuda.synchronize()
     ref = reference_f16(q, k, v, causal, -1, cos, sin)

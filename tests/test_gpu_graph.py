@@ -41,7 +41,7 @@ def _check_replays(fn, outs, n=3):
 
 
 def test_fp16_rope_prefill_graph(gpu):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log("[graph] fp16 prefill + rope")
     g = torch.Generator().manual_seed(30)
@@ -57,7 +57,7 @@ def test_fp16_rope_prefill_graph(gpu):
 
 
 def test_splitk_decode_graph(gpu):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log("[graph] split-K decode")
     g = torch.Generator().manual_seed(31)
@@ -71,7 +71,7 @@ def test_splitk_decode_graph(gpu):
 
 
 def test_quantized_int8_graph(gpu):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log("[graph] quantised int8 + rope")
     g = torch.Generator().manual_seed(32)

@@ -168,14 +168,14 @@ def test_int8_quantized_python_path(gpu, oracle_lib):
     """flash_attn_int8qk_quantized end to end: torch quantisers on the GPU, the
     kernel, the per-channel V rescale; checked against the oracle's emulation on
     the same quantised tensors and against fp attention (GQA ratio 4)."""
-    import rdnattention_amd
+    import rdnattention
 
     g = torch.Generator().manual_seed(2)
     b, hq, hkv, s, d = 1, 8, 2, 600, 128
     q = torch.randn(b, hq, s, d, generator=g).half()
     k = torch.randn(b, hkv, s, d, generator=g).half()
     v = torch.randn(b, hkv, s, d, generator=g).half()
-    out = rdnattention_amd.flash_attn_int8qk_quantized(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=True)
+    out = rdnattention.flash_attn_int8qk_quantized(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=True)
     torch.cuda.synchronize()
     qi, qsv = oracle.quant_pertoken(q.float().numpy())
     ki, ksv = oracle.quant_pertoken(k.float().numpy())
@@ -230,7 +230,7 @@ PERSISTENT_CASES = [
 def test_int8_persistent_workgroups_cover_every_tile(gpu, oracle_lib, case):
     """Output pre-filled with NaN: a row tile that no workgroup writes fails
     the finiteness check, one written wrongly fails the INT8 bar."""
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     name, b, hq, hkv, s, d, causal, window, vchan = case
     log(f"[int8 persistent] {name}")

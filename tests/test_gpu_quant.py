@@ -64,7 +64,7 @@ SHAPES = [(1, 4, 70, 64), (2, 3, 33, 128), (1, 2, 129, 96), (1, 1, 17, 32), (1, 
 @pytest.mark.parametrize("strided", [False, True], ids=["contig", "strided"])
 @pytest.mark.parametrize("shape", SHAPES, ids=[f"{s[2]}x{s[3]}" for s in SHAPES])
 def test_pertoken_bit_identical_to_torch(gpu, dtype, strided, shape):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"[quant] pertoken {shape} {dtype} strided={strided}")
     x = make_x(gpu, shape, dtype, 10, strided)
@@ -81,7 +81,7 @@ def test_pertoken_bit_identical_to_torch(gpu, dtype, strided, shape):
 @pytest.mark.parametrize("shape", SHAPES + [(1, 2, 5000, 128), (2, 1, 1, 64)],
                          ids=[f"{s[2]}x{s[3]}" for s in SHAPES + [(1, 2, 5000, 128), (2, 1, 1, 64)]])
 def test_perchannel_bit_identical_to_torch(gpu, dtype, strided, shape):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"[quant] perchannel {shape} {dtype} strided={strided}")
     x = make_x(gpu, shape, dtype, 11, strided)
@@ -96,7 +96,7 @@ def test_perchannel_bit_identical_to_torch(gpu, dtype, strided, shape):
 def test_public_quantisers_use_the_kernels(gpu):
     """quantize_int8_qk_pertoken / quantize_int8_perchannel_v on HIP tensors
     give the reference formulas' results."""
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     g = torch.Generator().manual_seed(12)
     q = torch.randn(2, 8, 100, 128, generator=g).half().to(gpu)
@@ -119,7 +119,7 @@ VCH_CASES = [(1, 4, 4, 200, 64, False, -1), (1, 8, 2, 300, 128, True, -1), (2, 4
 
 @pytest.mark.parametrize("case", VCH_CASES, ids=[f"b{c[0]}h{c[1]}kv{c[2]}s{c[3]}d{c[4]}" for c in VCH_CASES])
 def test_vchannel_kernel(gpu, case):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     b, hq, hkv, s, d, causal, window = case
     log(f"[quant] vchannel {case}")
@@ -153,7 +153,7 @@ def test_quantized_end_to_end_matches_reference_composition(gpu, hkv):
     """flash_attn_int8qk_quantized against the reference's composition
     (rdnattention/__init__.py:346-357): torch quantisers, flash_attn_int8qk
     with v_scale = 1, then out.float() * v_channel -> fp16."""
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"[quant] end to end hkv={hkv}")
     g = torch.Generator().manual_seed(14)
@@ -185,7 +185,7 @@ ROPE_SHAPES = [(1, 4, 70, 64), (2, 3, 33, 128), (1, 2, 300, 256), (1, 2, 40, 512
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
 @pytest.mark.parametrize("shape", ROPE_SHAPES, ids=[f"{s[2]}x{s[3]}" for s in ROPE_SHAPES])
 def test_pertoken_rope_quantiser(gpu, dtype, shape):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"[quant] pertoken rope {shape} {dtype}")
     b, h, s, d = shape
@@ -208,7 +208,7 @@ def test_pertoken_rope_quantiser(gpu, dtype, shape):
 
 
 def test_rope_quantiser_rejects_per_channel(gpu):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     x = torch.randn(1, 2, 16, 64, device=gpu)
     cos, sin = oracle.rope_tables(16, 64)
@@ -222,7 +222,7 @@ def test_quantized_rope_end_to_end(gpu, oracle_lib, causal, hkv):
     """flash_attn_int8qk_quantized with RoPE against the kernel-exact INT8
     emulation of the oracle-rotated, oracle-quantised inputs (INT8 bar, at the
     channel scales)."""
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"[quant] rope end to end causal={causal} hkv={hkv}")
     g = torch.Generator().manual_seed(16)

@@ -253,13 +253,13 @@ def test_f16_full_size_against_reference_library(gpu, ref, case):
 def test_int8_full_size_against_reference_library(gpu, ref):
     name, b, hq, hkv, s, d = "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128", 2, 32, 8, 8192, 128
     log(f"[ref-lib] full size {name}")
-    import rdnattention_amd
+    import rdnattention
 
     g = torch.Generator(device=gpu).manual_seed(zlib.crc32(name.encode()))
     q = torch.randn(b, hq, s, d, generator=g, device=gpu, dtype=torch.float16)
     k = torch.randn(b, hkv, s, d, generator=g, device=gpu, dtype=torch.float16)
     v = torch.randn(b, hkv, s, d, generator=g, device=gpu, dtype=torch.float16)
-    qi, ki, qsc, ksc = rdnattention_amd.quantize_int8_qk_pertoken(q, k)
+    qi, ki, qsc, ksc = rdnattention.quantize_int8_qk_pertoken(q, k)
     vsc = v.float().abs().max().item() / 127.0
     vi = torch.clamp(torch.round(v.float() / vsc), -127, 127).to(torch.int8)
     del q, k, v

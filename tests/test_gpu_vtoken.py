@@ -47,7 +47,7 @@ def _scales(case, rng):
 
 
 def _run(qi, ki, vi, qs, ks, causal, window, v_token=None):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     out = torch.full(qi.shape, float("nan"), dtype=torch.float16, device="cuda")
     dq = torch.from_numpy(qs).cuda() if isinstance(qs, np.ndarray) else qs
@@ -99,7 +99,7 @@ def test_vtoken_vs_emulation(gpu, case):
 @pytest.mark.gpu
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 def test_vtoken_quantized_end_to_end(gpu, causal):
-    import rdnattention_amd as ra
+    import rdnattention as ra
 
     log(f"vtoken end to end causal={causal}")
     g = torch.Generator().manual_seed(73)

@@ -1,7 +1,7 @@
 """Resource audit of every gfx950 kernel in the last build (CPU only).
 
-rdnattention_amd/_build.py records the compiler's kernel-resource-usage
-remarks in rdnattention_amd/lib/kernel_resources.json.  This test holds the
+rdnattention/_build.py records the compiler's kernel-resource-usage
+remarks in build/kernel_resources.json.  This test holds the
 kernels to what their launches assume (the reference audits its own tile
 choices against a VGPR cap, tests/head_dim_resources.py):
 
@@ -16,7 +16,7 @@ import re
 
 import pytest
 
-from rdnattention_amd import _build
+from rdnattention import _build
 
 LDS_LIMIT = 160 * 1024
 
