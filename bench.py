@@ -543,7 +543,60 @@ def pmc_summary(directory: str) -> int:
         return 1
     for (kern, ctr), (s, n) in sorted(acc.items()):
         print(f"{ctr:<28} dispatches={n:<5} mean={s / n:16.1f}  {kern[:110]}")
+    for line in pmc_derived(directory, {k: s / n for k, (s, n) in acc.items()}):
+        print(line)
     return 0
+
+
+def pmc_derived(directory: str, mean):
+    """Derived per-kernel figures from mean per-dispatch counters (and, when
+    a run_kernel_trace.csv is present, mean dispatch durations):
+      mfma_busy  SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x SIMDs):
+                 the share of SIMD cycles the matrix core is busy at the clock
+                 it ran at (the busy-cycle counter is 32 cycles per 32x32x16
+                 f16 or 32x32x32 i8 MFMA issued; GRBM_GUI_ACTIVE is summed
+                 over the XCDs);
+      sclk       GRBM_GUI_ACTIVE / XCDs cycles / mean duration;
+      valu/mfma  non-MFMA VALU instructions per MFMA instruction;
+      lds_conflict_per_inst  SQ_LDS_BANK_CONFLICT cycles per LDS instruction."""
+    simds, xcds = 1024, 8
+    for path in Path(directory).rglob("*agent_info.csv"):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Agent_Type") == "GPU" and int(row.get("Simd_Count", 0) or 0) > 0:
+                    simds = int(row["Simd_Count"])
+                    xcds = max(1, int(row.get("Num_Xcc", 1) or 1))
+    dur = {}
+    for path in Path(directory).rglob("*kernel_trace.csv"):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                s, n = dur.get(row["Kernel_Name"], (0.0, 0))
+                dur[row["Kernel_Name"]] = (s + int(row["End_Timestamp"]) - int(row["Start_Timestamp"]), n + 1)
+    out = []
+    for kern in sorted({k for k, _ in mean}):
+        def c(name):
+            return mean.get((kern, name))
+
+        items = []
+        busy, gui = c("SQ_VALU_MFMA_BUSY_CYCLES"), c("GRBM_GUI_ACTIVE")
+        gui = gui / xcds if gui else gui
+        if busy is not None and gui:
+            items.append(f"mfma_busy={busy / (gui * simds):.4f}")
+        if gui and kern in dur:
+            ns = dur[kern][0] / dur[kern][1]
+            items.append(f"sclk_mhz={gui / ns * 1e3:.0f}")
+        valu, mfma = c("SQ_INSTS_VALU"), c("SQ_INSTS_MFMA")
+        if valu is not None and mfma:
+            items.append(f"valu_non_mfma_per_mfma={(valu - mfma) / mfma:.2f}")
+        trans = c("SQ_INSTS_VALU_TRANS_F32")
+        if trans is not None and mfma:
+            items.append(f"trans_per_mfma={trans / mfma:.3f}")
+        conf, lds = c("SQ_LDS_BANK_CONFLICT"), c("SQ_INSTS_LDS")
+        if conf is not None and lds:
+            items.append(f"lds_conflict_cycles_per_inst={conf / lds:.4f}")
+        if items:
+            out.append(f"derived {kern[:90]}: " + " ".join(items))
+    return out
 
 
 # --------------------------------------------------------------------------- #

@@ -31,9 +31,13 @@ RDNA_API int32_t rdna_attention_forward_path(
 
 /* Exact int32 scores S = Q_i8 K_i8^T (GQA head map kv = h / (Hq/Hkv)),
  * written to `scores`, a contiguous int32 [batch, num_heads, seq_len,
- * key_seq_len] device buffer.  Uses the same int8 MFMA tiles as
- * rdna_attention_forward_int8qk's first GEMM.  No reference counterpart:
- * it exposes the scores so tests can check them bit for bit. */
+ * key_seq_len] device buffer.  Runs the INT8 attention kernel itself (its
+ * score-export instantiation: the same K tile staging, LDS layout, operand
+ * ring and v_mfma_i32_32x32x32_i8 sequence as rdna_attention_forward_int8qk's
+ * first GEMM) and writes its accumulators; softmax, P V and output are
+ * compiled out.  Key and query strides as for the forward (seq strides
+ * <= 2^24 elements).  No reference counterpart: it exposes the production
+ * kernel's scores so tests can check them bit for bit. */
 RDNA_API int32_t rdna_int8_qk_scores(
     const void* q, const void* k, int32_t* scores,
     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,

@@ -395,7 +395,8 @@ ORACLE_API int32_t oracle_int8_scores(const int8_t* q, const int8_t* k, int32_t*
 /* q_scale_vec: [B,Hq,Sq] or NULL (use q_scale); k_scale_vec: [B,Hkv,Sk] or   */
 /* NULL (use k_scale) -- the contiguous indexing of :410 and :287.           */
 /* v_token_vec ([B,Hkv,Sk], the library's per-token V extension; no          */
-/* reference counterpart): V row j becomes v'_j = fp16(v_j * fp16(vs_j)) and */
+/* reference counterpart): V row j becomes v'_j = fp16(sat(v_j * vs_j)),     */
+/* the product in fp32 saturated to +-65504 and rounded once to fp16, and    */
 /* O += (sum_j pq_j v'_j) * ((1/127) * v_scale), the sum in double.          */
 /* ------------------------------------------------------------------------ */
 typedef struct {
@@ -491,10 +492,11 @@ static void i8_task(void* vctx, int64_t task) {
                 }
                 const int8_t* vr = vb + j * c->D;
                 if (vtb) {
-                    /* v * fp16(vs) is exact in fp32 (8 x 11 bits): one rounding */
-                    const float vs16 = oracle_round_f16(vtb[j]);
+                    const float vs = vtb[j];
                     for (int64_t d = 0; d < c->D; d++) {
-                        pvd[d] += (double)pq[jj] * (double)oracle_round_f16((float)vr[d] * vs16);
+                        float x = (float)vr[d] * vs;
+                        x = x > 65504.0f ? 65504.0f : (x < -65504.0f ? -65504.0f : x);
+                        pvd[d] += (double)pq[jj] * (double)oracle_round_f16(x);
                     }
                 } else {
                     for (int64_t d = 0; d < c->D; d++) {

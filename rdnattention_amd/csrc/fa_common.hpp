@@ -352,32 +352,47 @@ __device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin
 // Q^T operand of one query row for the 32x32x16 MFMAs: out[s] = Q[row][16s + 8g .. +7],
 // RoPE-rotated with the table row of this position when `rope`, negated when `neg`, zero
 // when !valid. `qrow`, `cos_row` and `sin_row` must point at readable rows even when
-// !valid. Every load is issued before any is used, so the row costs one memory round
-// trip; with the RoPE loads inside a per-chunk branch the compiler waited for each
-// chunk's loads in turn.
-template <int NS>
+// !valid. Within a chunk of CH slices every load is issued before any is used, so a chunk
+// costs one memory round trip (with the RoPE loads inside a per-slice branch the compiler
+// waited for each slice's loads in turn); chunks bound the registers the tables hold
+// (a D = 512 row with all its tables live would need 384).
+template <int NS, int CH = NS>
 __device__ __forceinline__ void load_q_operand(h8 (&out)[NS], const _Float16* qrow, const float* cos_row,
                                                const float* sin_row, int g, bool valid, bool rope, bool neg) {
-    h8 x[NS];
 #pragma unroll
-    for (int s = 0; s < NS; s++) {
-        x[s] = *reinterpret_cast<const h8*>(qrow + 16 * s + 8 * g);
-    }
-    if (rope) {
-        f4 c[NS], sn[NS];
+    for (int s0 = 0; s0 < NS; s0 += CH) {
+        constexpr int n = CH; // the last chunk may be partial: slices s0 + s >= NS are skipped
+        h8 x[n];
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            c[s] = *reinterpret_cast<const f4*>(cos_row + 8 * s + 4 * g);
-            sn[s] = *reinterpret_cast<const f4*>(sin_row + 8 * s + 4 * g);
+        for (int s = 0; s < n; s++) {
+            if (s0 + s < NS) {
+                x[s] = *reinterpret_cast<const h8*>(qrow + 16 * (s0 + s) + 8 * g);
+            }
+        }
+        if (rope) {
+            f4 c[n], sn[n];
+#pragma unroll
+            for (int s = 0; s < n; s++) {
+                if (s0 + s < NS) {
+                    c[s] = *reinterpret_cast<const f4*>(cos_row + 8 * (s0 + s) + 4 * g);
+                    sn[s] = *reinterpret_cast<const f4*>(sin_row + 8 * (s0 + s) + 4 * g);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < n; s++) {
+                if (s0 + s < NS) {
+                    x[s] = rope8_cs(x[s], c[s], sn[s]);
+                }
+            }
         }
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            x[s] = rope8_cs(x[s], c[s], sn[s]);
+        for (int s = 0; s < n; s++) {
+            if (s0 + s < NS) {
+                out[s0 + s] = valid ? (neg ? -x[s] : x[s]) : h8{};
+            }
         }
-    }
-#pragma unroll
-    for (int s = 0; s < NS; s++) {
-        out[s] = valid ? (neg ? -x[s] : x[s]) : h8{};
+        // the next chunk's loads are not hoisted above this chunk's rotation
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 

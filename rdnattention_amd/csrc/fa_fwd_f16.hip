@@ -44,12 +44,16 @@ constexpr float kRescaleThreshold = 8.0f; // log2 units
 
 template <int D>
 struct PrefillCfg {
-    // K and V tiles are row-major [64 keys][D] in LDS with a 32-byte row pad:
-    // rows 0..7 then start in distinct 32-byte bank groups, which keeps both
-    // the ds_read_b128 of K and the 4-row ds_read_b64_tr_b16 of V conflict-free
-    static constexpr int LD = D + 16;
+    // K and V tiles are row-major [64 keys][D] in LDS (64 banks x 4 B).  K
+    // rows at D+8 halves: a 16-byte step mod 256 B puts the 16 rows of one
+    // ds_read_b128 pass in distinct banks.  V rows at a stride = 32 (mod 128)
+    // halves, a 64-byte step mod 256 B: the 4 rows x 64 B that the 32 lanes of
+    // a ds_read_b64_tr_b16 pass read are then distinct too
+    static constexpr int LD = D + 8;
+    static constexpr int LDV = D + ((32 - D % 128) + 128) % 128;
     static constexpr int TILE_ELEMS = kBN * LD;
-    static constexpr int BUF_ELEMS = 2 * TILE_ELEMS; // K then V
+    static constexpr int TILE_V_ELEMS = kBN * LDV;
+    static constexpr int BUF_ELEMS = TILE_ELEMS + TILE_V_ELEMS; // K then V
     static constexpr int NS = D / 16;                // QK^T reduction steps
     static constexpr int NDT = D / 32;               // O^T row tiles
     static constexpr int KCH = D / 8;                // 16-byte chunks per K/V row
@@ -125,7 +129,7 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
     // at key row 4g + j/4 (+8 for the second half of the slots), columns
     // 16*(lane/16 % 2) + 4*(j % 4) of the 32-column d tile
     const int j16 = lane & 15;
-    const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LD + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+    const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LDV + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
     float psum = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
@@ -140,9 +144,9 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
             const int u = 2 * kt + hh; // 16-key group: keys 16u + 4g + {0..3, 8..11}
 #pragma unroll
             for (int dt = 0; dt < C::NDT; dt++) {
-                const _Float16* base = vrow + (16 * u) * C::LD + 32 * dt;
+                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
                 h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LD);
+                h4 hi = lds_read_tr16(base + 8 * C::LDV);
                 h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 oacc[dt] = mfma_32x32x16_f16(a, pb[hh], oacc[dt]);
             }
@@ -222,7 +226,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
     // per-thread chunk of a tile: row e / KCH, 16-byte column e % KCH
     uint32_t koff[C::KT];
     uint32_t voff[C::KT];
-    int loff[C::KT];
+    int loff[C::KT];  // LDS element offset of the chunk in the K tile, -1 = none
+    int lvoff[C::KT]; // ... in the V tile
 #pragma unroll
     for (int it = 0; it < C::KT; it++) {
         const int e = tid + it * kThreads;
@@ -232,6 +237,7 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         koff[it] = (uint32_t)(((int64_t)row * p.k_ss + 8 * ch) * 2);
         voff[it] = (uint32_t)(((int64_t)row * p.v_ss + 8 * ch) * 2);
         loff[it] = ok ? row * C::LD + 8 * ch : -1;
+        lvoff[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
 
     // HBM -> registers for tile t.  The buffer resources are rebased to the
@@ -255,7 +261,7 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         for (int it = 0; it < C::KT; it++) {
             if (C::TASK % kThreads == 0 || loff[it] >= 0) {
                 *reinterpret_cast<h8*>(&sK[loff[it]]) = kreg[it];
-                *reinterpret_cast<h8*>(&sV[loff[it]]) = vreg[it];
+                *reinterpret_cast<h8*>(&sV[lvoff[it]]) = vreg[it];
             }
         }
     };
@@ -818,9 +824,15 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.Sq = a.Sq;
     p.Hkv = a.Hkv;
     p.ratio = a.Hq / a.Hkv;
-    p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
     const bool pp = a.D <= 128;
-    p.rows_per_wg = 32 * (pp ? kPPWaves : kWaves) / p.G;
+    if (a.D > kWideSplitMaxPairD) {
+        // the wave-pair split kernel: two pairs of waves, each pair 32 rows of one head
+        p.G = (p.ratio % 2 == 0) ? 2 : 1;
+        p.rows_per_wg = 64 / p.G;
+    } else {
+        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
+        p.rows_per_wg = 32 * (pp ? kPPWaves : kWaves) / p.G;
+    }
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
     p.n_head_groups = a.B * a.Hkv * p.groups_per_kv;

@@ -1,6 +1,6 @@
 // INT8 FlashAttention forward for gfx950: Q K^T on int8 MFMA
-// (v_mfma_i32_32x32x32_i8, exact int32 accumulation), P V on fp16 MFMA with
-// integer operands (exact), fp16 output.
+// (v_mfma_i32_32x32x32_i8, exact int32 accumulation), P V on fp16 MFMA,
+// fp16 output.
 //
 // Replaces the reference's forwardKernelInt8QK
 // (src/rdna/fa2_forward_int8qk.hip:229-495) and keeps its numeric scheme:
@@ -11,24 +11,38 @@
 //     m'  = max(m, max_j s_ij);  O *= 2^(m - m'),  l *= 2^(m - m')
 //     p   = 2^(s - m'),  l += sum p                  (unquantised p)
 //     pq  = min(127, round(p * 127))                 (P as integers 0..127)
-//     O  += sum_j pq_j v_j                           (exact integer products)
+//     O  += sum_j pq_j v_j
 //   out = O * v_scale / (127 l)  (0 when no key is visible)
 //
-// Deliberate differences, all below the INT8 tolerance: round() is
+// The running max m is exact per block, as the scheme requires (pq depends
+// on it).  O and l are instead kept relative to a lagging reference m_ref <=
+// m, raised only when m exceeds it by more than 2^8: each block's P enters
+// the P V product as pq * fp16(2^(m - m_ref)) (packed fp16 multiplies, one
+// rounding, values <= 127 * 256) and its row sum as sum p * that same factor,
+// so O / l is the scheme's ratio while the 64-accumulator rescale of O runs
+// only when the reference moves.  P V runs on fp16 MFMA: the products of
+// these fp16 P values and the int8 V values (exact in fp16) are exact in
+// fp32.
+//
+// Deliberate differences, all far below the INT8 tolerance: round() is
 // round-half-to-even (v_rndne_f32) where the reference calls lroundf (half
-// away from zero), 127 p is evaluated as 2^(s - m' + log2 127), and the per-
-// block v_scale/127 factor is applied once at the end.  pq * v products are
-// exact in fp16 MFMA (|pq| <= 127, |v| <= 127) and a block's sums stay below
-// 2^24, so P V on fp16 MFMA gives the same integers as the reference's int32
-// GEMM while O accumulates in fp32 without a per-block conversion pass.
+// away from zero), 127 p is evaluated as 2^(s - m' + log2 127), the per-block
+// v_scale/127 factor is applied once at the end, and P is scaled by the
+// reference factor above (relative rounding <= 2^-12 per element).
 //
 // Kernel structure is the FP16 ping-pong design (fa_fwd_f16.hip): 8 waves in
 // two groups alternating MFMA and VALU phases, S^T = K Q^T so a lane owns one
 // query column, and P^T going from the S accumulator straight into the B
 // operand of O^T = V^T P^T.  V is converted to fp16 while it is staged into
-// LDS and its V^T operands come from ds_read_b64_tr_b16 transpose reads.  The
-// grid is persistent (persistent_item), and O leaves through an LDS buffer as
-// whole-row non-temporal stores (store_o_tile).
+// LDS (a byte permute against the fp16 exponent of 1024, then one packed
+// subtract) and its V^T operands come from ds_read_b64_tr_b16 transpose
+// reads.  The grid is persistent (persistent_item), and O leaves through an
+// LDS buffer as whole-row non-temporal stores (store_o_tile).
+//
+// SCORES (a test instantiation): the same kernel with the softmax, P V and
+// output compiled out; every S^T accumulator block its first GEMM produces is
+// written to an int32 score buffer, so the tests can check the production
+// GEMM's scores bit for bit.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
@@ -62,6 +76,7 @@ struct Int8Params {
     const float* ksv; // [B, Hkv, Sk] or null
     const float* vch; // [B, Hkv, D] per-channel V scale or null
     const float* vtok; // [B, Hkv, Sk] per-token V scale (the VTOK kernel) or null
+    int32_t* scores;   // [B, Hq, Sq, Sk] int32 (the SCORES instantiation only)
     float q_scale, k_scale;
     float v_scale;
     float scale_log2e;
@@ -94,6 +109,7 @@ struct I8Cfg {
 
 constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
 constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
+constexpr float kI8RefThreshold = 8.0f;      // log2 units: P is scaled by at most 2^8 (127 * 256 < 65504)
 
 __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -101,44 +117,61 @@ __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(i4, x);
 }
 
-// 16 signed bytes -> two h8 (exact: every int8 is an fp16 integer)
+// 16 signed bytes -> two h8 (exact: every int8 is an fp16 integer).  Flipping
+// the sign bit gives u = v + 128 as an unsigned byte; a byte permute pairs each
+// u with the high byte 0x64, i.e. the fp16 value 1024 + u (exact: the ulp in
+// [1024, 2048) is 1), and one packed subtract of 1152 leaves v.  Five VALU
+// instructions per 4 values.
 __device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
+    const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    h2 r[8];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t u = (uint32_t)w[c] ^ 0x80808080u;
+        // byte selects: 0-3 pick bytes of u, 4 picks byte 0 of 0x64646464
+        const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+        const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+        r[2 * c] = __builtin_bit_cast(h2, p01) - off;
+        r[2 * c + 1] = __builtin_bit_cast(h2, p23) - off;
+    }
+    lo = {r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
+    hi = {r[4][0], r[4][1], r[5][0], r[5][1], r[6][0], r[6][1], r[7][0], r[7][1]};
+}
+
+// 16 signed bytes of one V row -> two h8 of fp16(sat(v * vs)): the product in
+// fp32 (v exact, vs as given), saturated to the fp16 range so that no V value
+// becomes infinite (a zero P times an infinite V would be NaN for every row
+// sharing the tile), then rounded once to fp16
+__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, float vs, h8& lo, h8& hi) {
     const i8x8 a = __builtin_bit_cast(i8x8, i2{w[0], w[1]});
     const i8x8 b = __builtin_bit_cast(i8x8, i2{w[2], w[3]});
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        lo[e] = (_Float16)a[e];
-        hi[e] = (_Float16)b[e];
+        lo[e] = (_Float16)__builtin_amdgcn_fmed3f((float)a[e] * vs, -65504.0f, 65504.0f);
+        hi[e] = (_Float16)__builtin_amdgcn_fmed3f((float)b[e] * vs, -65504.0f, 65504.0f);
     }
-}
-
-// 16 signed bytes of one V row -> two h8 of fp16(v * vs16), vs16 = fp16(vs):
-// the exact int8 -> fp16 conversion, then packed fp16 multiplies, each
-// product rounded once
-__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, _Float16 vs16, h8& lo, h8& hi) {
-    i8x16_to_h8x2(w, lo, hi);
-    const h8 s = {vs16, vs16, vs16, vs16, vs16, vs16, vs16, vs16};
-    lo *= s;
-    hi *= s;
 }
 
 // Scheme (the reference's, fa2_forward_int8qk.hip:281-382), per 64-key block b
 // aligned to key 0, with s_j = S_j * qs * ks_j * scale * log2(e):
-//   m_b  = max(m_{b-1}, max_j s_j),  corr = 2^(m_{b-1} - m_b)
+//   m_b  = max(m_{b-1}, max_j s_j)     (exact: pq below depends on it)
 //   y_j  = 127 * 2^(s_j - m_b)         (computed as 2^(s_j - m_b + log2 127))
-//   pq_j = round(y_j) in [0, 127]      (P: exact integers in fp16)
-//   l    = l * corr + sum_j y_j        (unquantised p, in units of 1/127)
-//   O    = O * corr + sum_j pq_j v_j   (exact integer products, fp32 sums)
+//   pq_j = round(y_j) in [0, 127]
+//   f_b  = fp16(2^(m_b - m_ref))       (m_ref <= m_b: raised, with O and l
+//                                       rescaled, only when m_b - m_ref > 8)
+//   l   += f_b * sum_j y_j              (unquantised p, in units of 1/127)
+//   O   += sum_j fp16(pq_j * f_b) v_j
 //   out  = O * v_scale / l
-// S runs on int8 MFMA (exact int32).  P V runs on fp16 MFMA, which is exact
-// for these integer operands and accumulates straight into fp32, so O needs
-// no per-block int32 -> fp32 conversion.
+// S runs on int8 MFMA (exact int32).  P V runs on fp16 MFMA and accumulates
+// straight into fp32, so O needs no per-block int32 -> fp32 conversion.
 //
 // VTOK (an extension; the reference has no per-token V scale): V row j is
 // dequantised by its own scale vs_j while it is staged,
-// v'_j = fp16(v_j * fp16(vs_j)), and P V runs on these fp16 values:
-// O = O * corr + sum_j pq_j v'_j.
-template <int D, bool VTOK>
+// v'_j = fp16(sat(v_j * vs_j)), and P V runs on these fp16 values.
+//
+// SCORES: the S^T accumulators of every computed key tile are written to
+// p.scores and nothing else is computed (test instantiation).
+template <int D, bool VTOK, bool SCORES>
 __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     using C = I8Cfg<D>;
     __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
@@ -219,7 +252,9 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         for (int dt = 0; dt < C::NDT; dt++) {
             oacc[dt] = f16x{};
         }
-        float m_run = -INFINITY, l_run = 0.0f;
+        // m_run: the scheme's exact running max; m_ref: the lagging reference
+        // O and l are kept relative to (m_ref <= m_run)
+        float m_run = -INFINITY, m_ref = -INFINITY, l_run = 0.0f;
         f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
         tsc[0] = f16x{};
         tsc[1] = f16x{};
@@ -279,7 +314,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     if (x >= 1 && x <= n) {
                         h8 lo, hi;
                         if constexpr (VTOK) {
-                            i8x16_to_h8x2_scaled(vreg[it], (_Float16)vsreg[it], lo, hi);
+                            i8x16_to_h8x2_scaled(vreg[it], vsreg[it], lo, hi);
                         } else {
                             i8x16_to_h8x2(vreg[it], lo, hi);
                         }
@@ -343,7 +378,24 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if constexpr (DO_S) {
+            if constexpr (DO_S && SCORES) {
+                // the two S^T blocks of this tile: lane holds query q, keys
+                // kt0 + 32 kt + 8 (e / 4) + 4 g + e % 4
+                if (q < p.Sq) {
+                    const int kt0 = (t_begin + i) * kI8BN;
+                    int32_t* srow = p.scores + (((int64_t)b * p.Hq + h) * p.Sq + q) * Sk;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int k0 = kt0 + 8 * (e >> 2) + 4 * g + (e & 3);
+                        if (k0 < Sk) {
+                            srow[k0] = acc0[e];
+                        }
+                        if (k0 + 32 < Sk) {
+                            srow[k0 + 32] = acc1[e];
+                        }
+                    }
+                }
+            } else if constexpr (DO_S) {
                 // dequantise here: the MFMA phase is the shorter one of the two
                 const float* ksl = sks[i & 1];
 #pragma unroll
@@ -362,7 +414,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             if (!wave_active) {
                 return;
             }
-            const bool do_pv = i >= 1 && cls_prev != 0;
+            const bool do_pv = !SCORES && i >= 1 && cls_prev != 0;
             int cls_now = 0;
             if (i < n) {
                 const int kt0 = (t_begin + i) * kI8BN;
@@ -380,10 +432,11 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             cls_prev = cls_now;
         };
 
-        // V(i): exact running max over the 64-key block, P as integers 0..127;
-        // O and l are rescaled whenever the max grows
+        // V(i): exact running max over the 64-key block, P as integers 0..127
+        // times the reference factor f; O and l are rescaled only when the
+        // reference moves
         auto phase_v = [&](int i) {
-            if (!wave_active || cls_prev == 0) {
+            if (SCORES || !wave_active || cls_prev == 0) {
                 return;
             }
             f16x t[2] = {tsc[0], tsc[1]};
@@ -419,17 +472,21 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 mx = fmaxf(mx, t[1][e]);
             }
             mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
-            const float m_new = fmaxf(m_run, mx);
-            const bool grow = m_new > m_run;
-            if (wave_any(grow)) {
-                const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
-                m_run = m_new;
+            m_run = fmaxf(m_run, mx);
+            const bool move = m_run > m_ref + kI8RefThreshold; // false while m_run = -inf
+            if (wave_any(move)) {
+                const float alpha = move ? fast_exp2(m_ref - m_run) : 1.0f; // m_ref = -inf -> 0
+                if (move) {
+                    m_ref = m_run;
+                }
                 l_run *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < C::NDT; dt++) {
                     oacc[dt] *= alpha;
                 }
             }
+            // m_ref = -inf only while m_run = -inf (no visible key yet: every p is 0)
+            const _Float16 f16 = (_Float16)(m_ref == -INFINITY ? 1.0f : fast_exp2(m_run - m_ref));
             const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
             float psum = 0.0f;
 #pragma unroll
@@ -441,7 +498,12 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
                 }
             }
-            l_run += psum;
+            const h8 fv = {f16, f16, f16, f16, f16, f16, f16, f16};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                pb[u] *= fv;
+            }
+            l_run = fmaf(psum, (float)f16, l_run);
         };
 
         if (n > 0) {
@@ -480,7 +542,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             }
         }
 
-        if (!wave_active) {
+        if (SCORES || !wave_active) {
             return;
         }
         // O = O^T * v_scale / l (times the per-channel V scales of this kv head
@@ -504,51 +566,18 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(64) void int8_scores_kernel(const int8_t* __restrict__ qp, const int8_t* __restrict__ kp,
-                                                        int32_t* __restrict__ out, int64_t q_sb, int64_t q_sh,
-                                                        int64_t q_ss, int64_t k_sb, int64_t k_sh, int64_t k_ss,
-                                                        int32_t Hq, int32_t Hkv, int32_t Sq, int32_t Sk) {
-    const int lane = threadIdx.x;
-    const int l32 = lane & 31, g = lane >> 5;
-    const int q0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
-    const int bh = blockIdx.z;
-    const int b = bh / Hq, h = bh - b * Hq;
-    const int kvh = h / (Hq / Hkv);
-    const int q = q0 + l32, key = k0 + l32;
-    i16x acc = {};
-#pragma unroll
-    for (int s = 0; s < D / 32; s++) {
-        i4 a = key < Sk ? *reinterpret_cast<const i4*>(kp + b * k_sb + kvh * k_sh + (int64_t)key * k_ss + 32 * s + 16 * g)
-                        : i4{};
-        i4 bq = q < Sq ? *reinterpret_cast<const i4*>(qp + b * q_sb + h * q_sh + (int64_t)q * q_ss + 32 * s + 16 * g)
-                       : i4{};
-        acc = mfma_32x32x32_i8(a, bq, acc);
-    }
-    if (q < Sq) {
-        int32_t* orow = out + ((int64_t)bh * Sq + q) * Sk;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int kk = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
-            if (kk < Sk) {
-                orow[kk] = acc[e];
-            }
-        }
-    }
-}
-
-template <int D, bool VTOK>
+template <int D, bool VTOK, bool SCORES>
 int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     // persistent: as many workgroups as the device holds at once, each
     // walking its share of the n_wg row tiles
     const int64_t resident =
-        resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D, VTOK>), kI8Threads, err);
+        resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D, VTOK, SCORES>), kI8Threads, err);
     if (resident <= 0) {
         return -1;
     }
     const int64_t grid = std::min(n_wg, resident);
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL((fa_fwd_int8<D, VTOK>), dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
+    hipLaunchKernelGGL((fa_fwd_int8<D, VTOK, SCORES>), dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -557,14 +586,14 @@ int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::stri
     return 0;
 }
 
-} // namespace
-
-int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
+// Kernel parameters and grid size of an INT8 launch (shared by the forward
+// and the score export).  Returns the number of row tiles, or -1 with `err`.
+int64_t int8_params(const AttnArgs& a, Int8Params& p, std::string& err) {
     if (a.ks[2] < 0 || a.vs[2] < 0 || a.ks[2] > (1 << 24) || a.vs[2] > (1 << 24)) {
         err = "key/value seq strides must be in [0, 2^24] elements";
         return -1;
     }
-    Int8Params p{};
+    p = Int8Params{};
     p.q = static_cast<const int8_t*>(a.q);
     p.k = static_cast<const int8_t*>(a.k);
     p.v = static_cast<const int8_t*>(a.v);
@@ -606,33 +635,52 @@ int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
         return -1;
     }
     p.n_items = (int32_t)n_wg;
+    return n_wg;
+}
+
+} // namespace
+
+int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
+    Int8Params p;
+    const int64_t n_wg = int8_params(a, p, err);
+    if (n_wg < 0) {
+        return -1;
+    }
     switch (a.D) {
-    case 64: return p.vtok ? launch_int8<64, true>(p, n_wg, stream, err) : launch_int8<64, false>(p, n_wg, stream, err);
+    case 64:
+        return p.vtok ? launch_int8<64, true, false>(p, n_wg, stream, err)
+                      : launch_int8<64, false, false>(p, n_wg, stream, err);
     case 128:
-        return p.vtok ? launch_int8<128, true>(p, n_wg, stream, err) : launch_int8<128, false>(p, n_wg, stream, err);
+        return p.vtok ? launch_int8<128, true, false>(p, n_wg, stream, err)
+                      : launch_int8<128, false, false>(p, n_wg, stream, err);
     default: break;
     }
     err = "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)";
     return -1;
 }
 
-int int8_scores(const AttnArgs& a, int32_t* scores, hipStream_t stream, std::string& err) {
-    dim3 grid((uint32_t)((a.Sq + 31) / 32), (uint32_t)((a.Sk + 31) / 32), (uint32_t)(a.B * a.Hq));
-    if (a.D == 64) {
-        hipLaunchKernelGGL(int8_scores_kernel<64>, grid, dim3(64), 0, stream, static_cast<const int8_t*>(a.q),
-                           static_cast<const int8_t*>(a.k), scores, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1],
-                           a.ks[2], a.Hq, a.Hkv, a.Sq, a.Sk);
-    } else {
-        hipLaunchKernelGGL(int8_scores_kernel<128>, grid, dim3(64), 0, stream, static_cast<const int8_t*>(a.q),
-                           static_cast<const int8_t*>(a.k), scores, a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1],
-                           a.ks[2], a.Hq, a.Hkv, a.Sq, a.Sk);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        err = hipGetErrorString(e);
+int int8_scores(const AttnArgs& in, int32_t* scores, hipStream_t stream, std::string& err) {
+    // the production kernel's SCORES instantiation: its K tiles, LDS layout,
+    // operand ring and MFMAs, with V staged from K and no output
+    AttnArgs a = in;
+    a.v = a.k;
+    a.vs[0] = a.ks[0], a.vs[1] = a.ks[1], a.vs[2] = a.ks[2];
+    a.o = nullptr;
+    a.causal = 0;
+    a.window = 0;
+    Int8Params p;
+    const int64_t n_wg = int8_params(a, p, err);
+    if (n_wg < 0) {
         return -1;
     }
-    return 0;
+    p.scores = scores;
+    switch (a.D) {
+    case 64: return launch_int8<64, false, true>(p, n_wg, stream, err);
+    case 128: return launch_int8<128, false, true>(p, n_wg, stream, err);
+    default: break;
+    }
+    err = "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)";
+    return -1;
 }
 
 #else // RDNATTENTION_NO_INT8: the reference's RDNATTENTION_ENABLE_INT8=OFF build (CMakeLists.txt:33)

@@ -60,7 +60,7 @@ enum class F16Path : int32_t { Auto = 0, Prefill = 1, SplitK = 2 };
 // FP16 forward (prefill tiles or split-K decode).  Returns 0 or sets `err`.
 int fwd_f16(const AttnArgs& a, F16Path path, hipStream_t stream, std::string& err);
 
-// INT8 forward (both GEMMs on int8 MFMA).  Returns 0 or sets `err`.
+// INT8 forward (Q K^T on int8 MFMA, P V on fp16 MFMA).  Returns 0 or sets `err`.
 int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err);
 
 // INT8 quantisation on the GPU (fa_quant.hip).  Returns 0 or sets `err`.

@@ -40,6 +40,10 @@ struct PrefillParams {
 int xcd_head_group_chunk(int n_head_groups, int64_t kv_bytes);
 
 // Large-head prefill (head_dim 288..512 in steps of 32), fa_fwd_f16_wide.hip.
+// Head dims above kWideSplitMaxPairD run the wave-pair split kernel, whose
+// workgroups hold 64 / G rows of G <= 2 heads (the launcher's PrefillParams
+// must be set up that way).
+constexpr int kWideSplitMaxPairD = 352;
 int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
 
 } // namespace rdna_amd

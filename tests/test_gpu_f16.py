@@ -246,8 +246,8 @@ def test_empty_key_sequence_outputs_zero(gpu):
 @pytest.mark.parametrize("d,s,window", [(256, 2048, 1024), (512, 1024, 1024), (416, 640, 256)])
 def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     """The large-head window workloads (two-sided window, RoPE, N(0, 0.5)) at
-    a size the oracle finishes quickly; D = 416 runs the two overlapping
-    column passes."""
+    a size the oracle finishes quickly; D = 416 runs the wave-pair split with
+    unequal halves (224 + 192 of the head dimension)."""
     q, k, v = seeded_inputs(4, 1, 2, 2, s, s, d, std=0.5)
     cos, sin = oracle.rope_tables(s, d)
     out = torch.empty_like(q, device=gpu)
@@ -256,6 +256,22 @@ def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     torch.cuda.synchronize()
     ref = reference_f16(q, k, v, False, window, cos, sin)
     assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_window{window}")
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(384, 6, 2), (416, 6, 3), (480, 8, 2), (512, 9, 3), (448, 4, 4)])
+def test_wave_pair_split_gqa(gpu, oracle_lib, d, hq, hkv):
+    """The wave-pair split kernel (D > 352) with one head per workgroup (odd
+    GQA ratios and MHA) and two (even ratios), causal with RoPE, ragged row
+    and key counts, equal and unequal halves of the head dimension."""
+    log(f"[split] d{d} hq{hq} hkv{hkv}")
+    q, k, v = seeded_inputs(15, 2, hq, hkv, 150, 213, d)
+    cos, sin = oracle.rope_tables(213, d)
+    out = torch.full_like(q, float("nan"), device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, True, -1, torch.from_numpy(cos).to(gpu),
+                       torch.from_numpy(sin).to(gpu)) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, True, -1, cos, sin)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"split d{d} gqa {hq}/{hkv}")
 
 
 @pytest.mark.parametrize("d", [288, 512])

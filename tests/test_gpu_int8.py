@@ -1,8 +1,10 @@
 """INT8 path on the GPU against the CPU oracle.
 
 Bars (from the build's acceptance criteria): the int32 Q K^T scores are
-bit-exact (through the rdna_int8_qk_scores export, which runs the same int8
-MFMA tiles as the attention kernel's first GEMM); the fp16 output is within
+bit-exact (through the rdna_int8_qk_scores export, which runs the attention
+kernel itself -- its SCORES instantiation, with the same K staging, LDS
+layout, operand ring and MFMAs -- and writes the first GEMM's accumulators);
+the fp16 output is within
 1e-2 max-abs of the kernel-exact CPU emulation of the same quantisation scheme
 (oracle.attention_int8, 64-key blocks with a running max, as
 src/rdna/fa2_forward_int8qk.hip:281-382); and within the reference gate's own
@@ -143,11 +145,21 @@ def test_int8_gate_cases(gpu, oracle_lib, case):
     assert rel < 5e-2, f"{name}: rel_rms {rel:.3e} vs the gate's emulation"
 
 
-@pytest.mark.parametrize("b,hq,hkv,sq,sk,d", [(1, 2, 2, 70, 90, 64), (2, 8, 2, 33, 130, 128), (1, 4, 1, 1, 200, 128)])
+@pytest.mark.parametrize("b,hq,hkv,sq,sk,d", [(1, 2, 2, 70, 90, 64), (2, 8, 2, 33, 130, 128), (1, 4, 1, 1, 200, 128),
+                                               (2, 32, 8, 300, 333, 128), (1, 4, 4, 257, 65, 64),
+                                               (1, 8, 2, 600, 1000, 128)])
 def test_int8_scores_bit_exact(gpu, oracle_lib, b, hq, hkv, sq, sk, d):
+    """Ragged key counts (not multiples of the 64-key tile), several row tiles
+    per head group (the persistent grid's walk), GQA ratios 1-4, and rows of
+    +-127 that reach the extreme sums +-127^2 D."""
+    log(f"[int8 scores] b{b} hq{hq} hkv{hkv} sq{sq} sk{sk} d{d}")
     rng = np.random.default_rng(7)
     qi = rng.integers(-127, 128, (b, hq, sq, d), dtype=np.int8)
     ki = rng.integers(-127, 128, (b, hkv, sk, d), dtype=np.int8)
+    if sq > 2 and sk > 2:
+        qi[-1, -1, 1] = 127
+        ki[-1, -1, -1] = -127
+        ki[-1, -1, 1] = 127
     qi[0, 0, 0] = 127
     ki[0, 0, 0] = 127
     if sq > 1:

@@ -125,3 +125,37 @@ def test_vtoken_quantized_end_to_end(gpu, causal):
     mx, mean, rel = errors(out.float().cpu().numpy(), fp)
     log(f"  vs fp attention rel_rms={rel:.3e}")
     assert rel < 5e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vs0", [1.0e6, 1.0e-7])
+def test_vtoken_extreme_scales(gpu, vs0):
+    """A V row whose scale drives v * vs past fp16 (1e6: saturates to
+    +-65504) or into fp16 subnormals (1e-7).  Nothing may become NaN or
+    infinite -- a masked key times an infinite V would poison every row of its
+    tile --, rows that cannot see key 0 (window 2: |i - j| <= 1) must equal the
+    run with vs_0 = 1 bit for bit, and causal row 0 (key 0 only) is v'_0,
+    within fp16 rounding of the oracle's value."""
+    log(f"vtoken extreme scale {vs0:g}")
+    rng = np.random.default_rng(74)
+    s, d = 24, 64
+    qi = rng.integers(-127, 128, (1, 2, s, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (1, 1, s, d), dtype=np.int8)
+    vi = rng.integers(-127, 128, (1, 1, s, d), dtype=np.int8)
+    vi[0, 0, 0, :8] = 127
+    vi[0, 0, 0, 8:16] = -127
+    vt = rng.uniform(0.01, 0.03, (1, 1, s)).astype(np.float32)
+    vt[0, 0, 0] = vs0
+    dq, dk, dv = (torch.from_numpy(x).cuda() for x in (qi, ki, vi))
+    got = _run(dq, dk, dv, 0.01, 0.01, True, -1, v_token=vt).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = oracle.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, causal=True, v_token=vt)
+    np.testing.assert_allclose(got[0, :, 0], ref[0, :, 0], rtol=2e-3, atol=1e-9)
+    mx, _, _ = errors(got[:, :, 1:], ref[:, :, 1:])
+    assert mx <= I8_MAX_ABS * max(1.0, float(np.abs(ref[:, :, 1:]).max())), mx
+    w = _run(dq, dk, dv, 0.01, 0.01, False, 2, v_token=vt)
+    vt1 = vt.copy()
+    vt1[0, 0, 0] = 1.0
+    w1 = _run(dq, dk, dv, 0.01, 0.01, False, 2, v_token=vt1)
+    assert torch.isfinite(w.float()).all()
+    assert torch.equal(w[:, :, 2:].view(torch.int16), w1[:, :, 2:].view(torch.int16))

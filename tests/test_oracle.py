@@ -425,6 +425,36 @@ def test_int8_vtoken_ones_and_constant_power_of_two(oracle_lib):
         oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 0.125, window=40))
 
 
+@pytest.mark.parametrize("vs0", [1.0e6, 1.0e-7])
+def test_int8_vtoken_extreme_scales(oracle_lib, vs0):
+    """One V row with a scale far outside the usual range: 1e6 drives v * vs
+    beyond fp16 (it saturates to +-65504, never inf), 1e-7 into fp16
+    subnormals.  Causal row 0 sees key 0 only, so its output is v'_0 itself:
+    checked against numpy's fp16 rounding of the saturated fp32 product.
+    Rows that cannot see key 0 (window 2: |i - j| <= 1) are bit-identical to a
+    run with vs_0 = 1, and nothing is NaN or infinite."""
+    rng = np.random.default_rng(64)
+    sq = sk = 24
+    qi = rng.integers(-127, 128, (1, 2, sq, 64), dtype=np.int8)
+    ki = rng.integers(-127, 128, (1, 1, sk, 64), dtype=np.int8)
+    vi = rng.integers(-127, 128, (1, 1, sk, 64), dtype=np.int8)
+    vi[0, 0, 0, :8] = 127
+    vi[0, 0, 0, 8:16] = -127
+    vt = rng.uniform(0.01, 0.03, (1, 1, sk)).astype(np.float32)
+    vt[0, 0, 0] = vs0
+    out = oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, causal=True, v_token=vt)
+    assert np.isfinite(out).all()
+    want = np.clip(vi[0, 0, 0].astype(np.float32) * np.float32(vs0), -65504, 65504).astype(np.float16)
+    np.testing.assert_array_equal(out[0, :, 0], np.broadcast_to(want.astype(np.float32), (2, 64)))
+    w = oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, window=2, v_token=vt)
+    vt1 = vt.copy()
+    vt1[0, 0, 0] = 1.0
+    w1 = oracle_lib.attention_int8(qi, ki, vi, 0.01, 0.01, 1.0, window=2, v_token=vt1)
+    assert np.isfinite(w).all()
+    np.testing.assert_array_equal(w[:, :, 2:], w1[:, :, 2:])
+    assert not np.array_equal(w[:, :, :2], w1[:, :, :2])
+
+
 def test_int8_vtoken_close_to_fp_attention(oracle_lib):
     """Per-token V quantisation approximates fp attention to the reference
     gate's bar (rel_rms < 5e-2)."""

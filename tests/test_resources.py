@@ -26,6 +26,7 @@ WAVES_PER_SIMD = {
     "fa_fwd_int8": 2,
     "fa_fwd_f16_prefill": 1,
     "fa_fwd_f16_wide": 1,
+    "fa_fwd_f16_wsplit": 1,
     "fa_fwd_f16_decode": 1,
 }
 
@@ -61,7 +62,8 @@ def test_occupancy_fits_the_workgroup(kernels):
         if need is not None:
             assert k["waves_per_simd"] >= need, (k["kernel"], k["waves_per_simd"], need)
             checked += 1
-    assert checked >= 4 + 4 + 8 + 3 + 2
+    # pp 4, prefill 4, wide 3 + wsplit 5, decode 3, int8 4 (+ 2 score-export instantiations)
+    assert checked >= 4 + 4 + 3 + 5 + 3 + 4
 
 
 def test_every_dispatched_head_dim_is_compiled(kernels):
@@ -74,8 +76,10 @@ def test_every_dispatched_head_dim_is_compiled(kernels):
         assert has("fa_fwd_f16_pp", d), d
     for d in (160, 192, 224, 256):
         assert has("fa_fwd_f16_prefill", d), d
-    for d in range(288, 513, 32):
+    for d in (288, 320, 352):
         assert has("fa_fwd_f16_wide", d), d
+    for d in range(384, 513, 32):
+        assert has("fa_fwd_f16_wsplit", d), d
     for d in (32, 64, 128):
         assert has("fa_fwd_f16_decode", d), d
     for d in (64, 128):
