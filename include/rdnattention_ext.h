@@ -29,6 +29,29 @@ RDNA_API int32_t rdna_attention_forward_path(
     float scale, int32_t causal, int32_t has_rope, int32_t window_size,
     int32_t path, void* hip_stream);
 
+/* rdna_attention_forward() for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No reference counterpart: the reference needs no scratch.
+ * Same arguments, results and return codes as rdna_attention_forward(); the
+ * scratch that path takes -- the RoPE-rotated K copy (B*Hkv*Sk*D fp16) and
+ * the split-K decode partials -- comes from a static 64 MiB device array the
+ * library holds on each GPU it runs on, so the call makes no hipMalloc,
+ * hipFree or pool allocation.  A call needing more than 64 MiB of scratch
+ * returns -3 ("... bytes of scratch ...") before launching anything.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on a GPU
+ * (different streams, not ordered) race. */
+RDNA_API int32_t rdna_attention_forward_noalloc(
+    const void* q, const void* k, const void* v, void* output,
+    const void* rot_cos, const void* rot_sin,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_s,
+    int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_s,
+    int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_s,
+    int64_t o_stride_b, int64_t o_stride_h, int64_t o_stride_s,
+    uint32_t batch_size, uint32_t num_heads, uint32_t num_kv_heads,
+    uint32_t seq_len, uint32_t key_seq_len, uint32_t head_dim,
+    float scale, int32_t causal, int32_t has_rope, int32_t window_size,
+    void* hip_stream);
+
 /* Exact int32 scores S = Q_i8 K_i8^T (GQA head map kv = h / (Hq/Hkv)),
  * written to `scores`, a contiguous int32 [batch, num_heads, seq_len,
  * key_seq_len] device buffer.  Runs the INT8 attention kernel itself (its

@@ -105,6 +105,11 @@ def _lib_handle():
         lib.rdna_attention_forward.restype = _I32
         lib.rdna_attention_forward_path.argtypes = _FWD_ARGS + [_I32, _VP]
         lib.rdna_attention_forward_path.restype = _I32
+        try:  # absent from libraries built before it existed (RDNATTENTION_LIB may name one)
+            lib.rdna_attention_forward_noalloc.argtypes = _FWD_ARGS + [_VP]
+            lib.rdna_attention_forward_noalloc.restype = _I32
+        except AttributeError:
+            pass
         lib.rdna_attention_forward_int8qk.argtypes = _I8_ARGS
         lib.rdna_attention_forward_int8qk.restype = _I32
         lib.rdna_attention_forward_int8qk_vchannel.argtypes = _I8_ARGS[:-3] + [_VP] + _I8_ARGS[-3:]

@@ -14,6 +14,7 @@
 #include "rdnattention.hpp"
 #include "rdnattention_ext.h"
 #include "fa_host.hpp"
+#include "fa_internal.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -82,7 +83,7 @@ int32_t forward_f16_impl(const void* q, const void* k, const void* v, void* outp
                          int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb, int64_t osh, int64_t oss,
                          uint32_t B, uint32_t Hq, uint32_t Hkv, uint32_t Sq, uint32_t Sk, uint32_t D, float scale,
                          int32_t causal, int32_t has_rope, int32_t window, F16Path path, void* stream,
-                         std::string& err) {
+                         std::string& err, bool noalloc = false) {
     if (!head_dim_f16_ok(D)) {
         err = "unsupported head_dim (multiples of 32 from 32 to 512)";
         return -1;
@@ -124,7 +125,26 @@ int32_t forward_f16_impl(const void* q, const void* k, const void* v, void* outp
     a.causal = causal != 0 ? 1 : 0;
     a.has_rope = has_rope != 0 ? 1 : 0;
     a.window = window > 0 ? window : 0;
-    return rdna_amd::fwd_f16(a, path, static_cast<hipStream_t>(stream), err);
+    if (!noalloc) {
+        return rdna_amd::fwd_f16(a, path, static_cast<hipStream_t>(stream), err);
+    }
+    // every scratch buffer from the static array; sized before any launch
+    const int64_t need = rdna_amd::fwd_f16_scratch_bytes(a, path, err);
+    if (need < 0) {
+        return -1;
+    }
+    if ((uint64_t)need > rdna_amd::kNoAllocBytes) {
+        err = "this call needs " + std::to_string(need) +
+              " bytes of scratch (RoPE-rotated K copy and/or split-K partials); the no-allocation entry point "
+              "provides " +
+              std::to_string(rdna_amd::kNoAllocBytes) + " bytes per device";
+        return -1;
+    }
+    rdna_amd::ScratchRegion region;
+    if (rdna_amd::noalloc_region(region, err) != 0) {
+        return -1;
+    }
+    return rdna_amd::fwd_f16(a, path, static_cast<hipStream_t>(stream), err, &region);
 }
 
 int32_t forward_i8_impl(const void* q, const void* k, const void* v, void* output, int64_t qsb, int64_t qsh,
@@ -218,6 +238,27 @@ RDNA_API int32_t rdna_attention_forward(const void* q, const void* k, const void
                               k_stride_h, k_stride_s, v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h,
                               o_stride_s, batch_size, num_heads, num_kv_heads, seq_len, key_seq_len, head_dim,
                               scale, causal, has_rope, window_size, F16Path::Auto, hip_stream, err);
+    if (rc != 0) {
+        set_error("Attention (fp16) failed: %s", err);
+        return -3;
+    }
+    return 0;
+}
+
+RDNA_API int32_t rdna_attention_forward_noalloc(const void* q, const void* k, const void* v, void* output,
+                                                const void* rot_cos, const void* rot_sin, int64_t q_stride_b,
+                                                int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b,
+                                                int64_t k_stride_h, int64_t k_stride_s, int64_t v_stride_b,
+                                                int64_t v_stride_h, int64_t v_stride_s, int64_t o_stride_b,
+                                                int64_t o_stride_h, int64_t o_stride_s, uint32_t batch_size,
+                                                uint32_t num_heads, uint32_t num_kv_heads, uint32_t seq_len,
+                                                uint32_t key_seq_len, uint32_t head_dim, float scale, int32_t causal,
+                                                int32_t has_rope, int32_t window_size, void* hip_stream) {
+    std::string err;
+    int rc = forward_f16_impl(q, k, v, output, rot_cos, rot_sin, q_stride_b, q_stride_h, q_stride_s, k_stride_b,
+                              k_stride_h, k_stride_s, v_stride_b, v_stride_h, v_stride_s, o_stride_b, o_stride_h,
+                              o_stride_s, batch_size, num_heads, num_kv_heads, seq_len, key_seq_len, head_dim,
+                              scale, causal, has_rope, window_size, F16Path::Auto, hip_stream, err, true);
     if (rc != 0) {
         set_error("Attention (fp16) failed: %s", err);
         return -3;

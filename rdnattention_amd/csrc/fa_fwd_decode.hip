@@ -402,7 +402,34 @@ bool splitk_supported(const AttnArgs& a) {
     return (a.D == 32 || a.D == 64 || a.D == 128) && M <= 32;
 }
 
-int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err) {
+int splitk_plan(const AttnArgs& a, int& splits, int& keys_per_split, std::string& err) {
+    // splits: one round of workgroups over the device (as many as it holds at
+    // once: one per CU at D = 128, where the LDS ring is 128 KB), each split a
+    // whole number of 4-wave tile rounds. Measured on the B=16 Hkv=8
+    // Sk=32768 cache: 256 workgroups stream 1-4 % faster than 512 and
+    // 4-14 % faster than 1024 or 2048; uneven counts (384, 768) are slower.
+    const int n_bkv = a.B * a.Hkv;
+    const int round = kDecWaves * kDecTile;
+    const int max_splits = std::max(1, (a.Sk + round - 1) / round);
+    const int64_t resident = a.D == 32 ? decode_resident<32>(err)
+                                       : (a.D == 64 ? decode_resident<64>(err) : decode_resident<128>(err));
+    if (resident <= 0) {
+        return -1;
+    }
+    const int n = (int)std::max<int64_t>(1, std::min<int64_t>(max_splits, (resident + n_bkv - 1) / n_bkv));
+    int kps = (a.Sk + n - 1) / n;
+    kps = std::max(round, (kps + round - 1) / round * round);
+    splits = std::max(1, (a.Sk + kps - 1) / kps);
+    keys_per_split = kps;
+    return 0;
+}
+
+size_t splitk_partial_bytes(const AttnArgs& a, int splits) {
+    const size_t n_part = (size_t)a.B * a.Hkv * splits * ((a.Hq / a.Hkv) * a.Sq);
+    return n_part * (a.D + 2) * sizeof(float);
+}
+
+int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err, ScratchRegion* region) {
     if (!splitk_supported(a)) {
         err = "split-K path needs head_dim in {32, 64, 128} and (num_heads / num_kv_heads) * seq_len <= 32";
         return -1;
@@ -431,29 +458,19 @@ int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::stri
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};
     p.rope_q = rope_q ? 1 : 0;
 
-    // splits: one round of workgroups over the device (as many as it holds at
-    // once: one per CU at D = 128, where the LDS ring is 128 KB), each split a
-    // whole number of 4-wave tile rounds. Measured on the B=16 Hkv=8
-    // Sk=32768 cache: 256 workgroups stream 1-4 % faster than 512 and
-    // 4-14 % faster than 1024 or 2048; uneven counts (384, 768) are slower.
     const int n_bkv = a.B * a.Hkv;
-    const int round = kDecWaves * kDecTile;
-    const int max_splits = std::max(1, (a.Sk + round - 1) / round);
-    const int64_t resident = a.D == 32 ? decode_resident<32>(err)
-                                       : (a.D == 64 ? decode_resident<64>(err) : decode_resident<128>(err));
-    if (resident <= 0) {
+    int splits = 0, kps = 0;
+    if (splitk_plan(a, splits, kps, err) != 0) {
         return -1;
     }
-    int splits = (int)std::max<int64_t>(1, std::min<int64_t>(max_splits, (resident + n_bkv - 1) / n_bkv));
-    int kps = (a.Sk + splits - 1) / splits;
-    kps = std::max(round, (kps + round - 1) / round * round);
-    splits = std::max(1, (a.Sk + kps - 1) / kps);
     p.splits = splits;
     p.keys_per_split = kps;
 
-    StreamScratch ws;
+    // every partial is written by its split's workgroup before the combine
+    // reads it, so the buffer needs no clearing
+    StreamScratch ws(region);
     const size_t n_part = (size_t)n_bkv * splits * p.M;
-    if (ws.alloc(n_part * (a.D + 2) * sizeof(float), stream, err) != 0) {
+    if (ws.alloc(splitk_partial_bytes(a, splits), stream, err) != 0) {
         return -1;
     }
     p.part_o = static_cast<float*>(ws.ptr);

@@ -878,7 +878,23 @@ bool prefer_splitk(const AttnArgs& a) {
     return splitk_supported(a) && a.Sk >= 512;
 }
 
-int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& err) {
+int64_t fwd_f16_scratch_bytes(const AttnArgs& a, F16Path path, std::string& err) {
+    const bool splitk = path == F16Path::SplitK || (path == F16Path::Auto && prefer_splitk(a));
+    size_t bytes = 0;
+    if (a.has_rope && a.Sk > 0) {
+        bytes += region_bytes((size_t)a.B * a.Hkv * a.Sk * a.D * sizeof(_Float16));
+    }
+    if (splitk && splitk_supported(a)) {
+        int splits = 0, kps = 0;
+        if (splitk_plan(a, splits, kps, err) != 0) {
+            return -1;
+        }
+        bytes += region_bytes(splitk_partial_bytes(a, splits));
+    }
+    return (int64_t)bytes;
+}
+
+int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& err, ScratchRegion* region) {
     AttnArgs a = in;
     // K/V rows are addressed with 32-bit byte offsets inside a 64-key tile
     if (a.ks[2] < 0 || a.vs[2] < 0 || a.ks[2] > kMaxSeqStride || a.vs[2] > kMaxSeqStride) {
@@ -886,7 +902,7 @@ int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& e
         return -1;
     }
     const bool splitk = path == F16Path::SplitK || (path == F16Path::Auto && prefer_splitk(a));
-    StreamScratch krot;
+    StreamScratch krot(region);
     if (a.has_rope && a.Sk > 0) {
         const size_t bytes = (size_t)a.B * a.Hkv * a.Sk * a.D * sizeof(_Float16);
         if (krot.alloc(bytes, stream, err) != 0 || rope_rotate_k(a, krot.ptr, stream, err) != 0) {
@@ -897,7 +913,7 @@ int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& e
         a.ks[1] = (int64_t)a.Sk * a.D;
         a.ks[2] = a.D;
     }
-    return splitk ? fwd_f16_splitk(a, a.has_rope != 0, stream, err)
+    return splitk ? fwd_f16_splitk(a, a.has_rope != 0, stream, err, region)
                   : fwd_f16_prefill(a, a.has_rope != 0, stream, err);
 }
 

@@ -57,8 +57,17 @@ struct QuantArgs {
 // Kernel paths the FP16 dispatcher can take.
 enum class F16Path : int32_t { Auto = 0, Prefill = 1, SplitK = 2 };
 
+struct ScratchRegion;
+
 // FP16 forward (prefill tiles or split-K decode).  Returns 0 or sets `err`.
-int fwd_f16(const AttnArgs& a, F16Path path, hipStream_t stream, std::string& err);
+// With `region`, every scratch buffer (the RoPE-rotated K copy, the split-K
+// partials) is carved from it and nothing is allocated; the caller first
+// checks fwd_f16_scratch_bytes against its size.
+int fwd_f16(const AttnArgs& a, F16Path path, hipStream_t stream, std::string& err, ScratchRegion* region = nullptr);
+
+// Scratch bytes fwd_f16 takes for these arguments (each buffer 256-byte
+// aligned), or -1 with `err`.
+int64_t fwd_f16_scratch_bytes(const AttnArgs& a, F16Path path, std::string& err);
 
 // INT8 forward (Q K^T on int8 MFMA, P V on fp16 MFMA).  Returns 0 or sets `err`.
 int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err);

@@ -11,19 +11,47 @@
 
 namespace rdna_amd {
 
-// Stream-ordered scratch memory: allocated with hipMallocAsync on the
-// caller's stream and released with hipFreeAsync on the same stream when the
-// object goes out of scope, i.e. after every kernel that uses it has been
-// enqueued.  Safe across concurrent streams and under graph capture.
+// A fixed device region that scratch buffers are carved from instead of
+// being allocated (the no-allocation entry point's static array): `used`
+// bytes of `bytes` at `base` are taken, each buffer 256-byte aligned.
+struct ScratchRegion {
+    char* base = nullptr;
+    size_t bytes = 0;
+    size_t used = 0;
+};
+
+// Bytes a buffer of `bytes` takes from a ScratchRegion (256-byte aligned).
+constexpr size_t region_bytes(size_t bytes) {
+    return (bytes + 255) / 256 * 256;
+}
+
+// Scratch memory for one call.  Without a region: allocated with
+// hipMallocFromPoolAsync (hipMallocAsync under graph capture) on the caller's
+// stream and released with hipFreeAsync on the same stream when the object
+// goes out of scope, i.e. after every kernel that uses it has been enqueued;
+// safe across concurrent streams and under graph capture.  With a region:
+// carved from it, nothing allocated or freed (the caller has checked that it
+// fits).
 struct StreamScratch {
     void* ptr = nullptr;
     hipStream_t stream = nullptr;
+    ScratchRegion* region = nullptr;
+    explicit StreamScratch(ScratchRegion* r = nullptr) : region(r) {}
     int alloc(size_t bytes, hipStream_t s, std::string& err);
-    StreamScratch() = default;
     StreamScratch(const StreamScratch&) = delete;
     StreamScratch& operator=(const StreamScratch&) = delete;
     ~StreamScratch();
 };
+
+// Size of the no-allocation entry point's static scratch array per device
+// (64 MiB): room for a RoPE-rotated K copy of B * Hkv * Sk * D fp16 values
+// up to 2^25 (a 4 x 8 x 4096 x 128 K is 2^24) together with split-K partials.
+constexpr size_t kNoAllocBytes = size_t(64) << 20;
+
+// The no-allocation entry point's region on the current device: the
+// library's static scratch array (fa_noalloc.hip), its device address looked
+// up once per device.  0, or -1 with `err`.
+int noalloc_region(ScratchRegion& r, std::string& err);
 
 // Rotates K ([B, Hkv, Sk, D] with a.ks strides) into `dst`, contiguous
 // [B, Hkv, Sk, D], with the tables a.rot_cos / a.rot_sin.
@@ -50,8 +78,16 @@ class KernelTimerGuard {
 // compute unit. Cached per device and kernel; <= 0 with `err` set on failure.
 int64_t resident_workgroups(const void* kernel, int threads, std::string& err);
 
-// Launchers.
+// Launchers.  `region`, when given, supplies every scratch buffer.
 int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err);
-int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err);
+int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::string& err,
+                   ScratchRegion* region = nullptr);
+
+// Split-K plan of a decode launch: key splits and keys per split.  0, or -1
+// with `err` (occupancy query failed).
+int splitk_plan(const AttnArgs& a, int& splits, int& keys_per_split, std::string& err);
+
+// Bytes of the split-K partials (per split and query row: O in fp32 plus m, l).
+size_t splitk_partial_bytes(const AttnArgs& a, int splits);
 
 } // namespace rdna_amd

@@ -92,6 +92,17 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
     if (bytes == 0) {
         return 0;
     }
+    if (region != nullptr) {
+        const size_t take = region_bytes(bytes);
+        if (region->used + take > region->bytes) {
+            err = "scratch region exhausted (" + std::to_string(region->used + take) + " of " +
+                  std::to_string(region->bytes) + " bytes)";
+            return -1;
+        }
+        ptr = region->base + region->used;
+        region->used += take;
+        return 0;
+    }
     // Under graph capture the allocation becomes a memory node the graph
     // owns: take it with hipMallocAsync (the device's default pool), which
     // graph capture supports; otherwise from the retaining pool.
@@ -119,7 +130,7 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
 }
 
 StreamScratch::~StreamScratch() {
-    if (ptr != nullptr) {
+    if (ptr != nullptr && region == nullptr) {
         (void)hipFreeAsync(ptr, stream);
     }
 }
