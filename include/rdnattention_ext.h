@@ -29,6 +29,14 @@ RDNA_API int32_t rdna_attention_forward_path(
     float scale, int32_t causal, int32_t has_rope, int32_t window_size,
     int32_t path, void* hip_stream);
 
+/* Releases the device memory the library keeps for reuse: the freed scratch
+ * blocks (RoPE-rotated K copies, split-K partials, quantiser partials) its
+ * per-device pools retain, up to 256 MiB per device, between calls.  Safe at
+ * any time; memory still in use by enqueued work is not released.  No
+ * reference counterpart (the reference allocates nothing).  Returns 0, or -3
+ * with rdna_get_error() set. */
+RDNA_API int32_t rdna_scratch_trim(void);
+
 /* rdna_attention_forward() for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No reference counterpart: the reference needs no scratch.

@@ -120,6 +120,11 @@ def _lib_handle():
         lib.rdna_quantize_int8.restype = _I32
         lib.rdna_int8_qk_scores.argtypes = [_VP] * 3 + [_I64] * 6 + [_U32] * 6 + [_VP]
         lib.rdna_int8_qk_scores.restype = _I32
+        try:  # absent from libraries built before it existed
+            lib.rdna_scratch_trim.argtypes = []
+            lib.rdna_scratch_trim.restype = _I32
+        except AttributeError:
+            pass
         lib.rdna_kernel_timer_enable.argtypes = [_I32]
         lib.rdna_kernel_timer_enable.restype = _I32
         lib.rdna_kernel_timer_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]
@@ -402,6 +407,15 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
         result = _lib_handle().rdna_attention_forward_int8qk_vchannel(*args, v_channel.data_ptr(), *tail)
     if result != 0:
         raise RDNAttentionError(f"attention_int8_forward_into failed: {last_error()}")
+
+
+def trim_scratch() -> None:
+    """Returns the scratch memory the library keeps for reuse on each device
+    (up to 256 MiB per device: freed RoPE-rotated K copies and split-K
+    partials) to the device, e.g. before handing memory to another
+    allocator.  An extension; the reference allocates nothing."""
+    if _lib_handle().rdna_scratch_trim() != 0:
+        raise RDNAttentionError(f"trim_scratch failed: {last_error()}")
 
 
 class KernelTimer:

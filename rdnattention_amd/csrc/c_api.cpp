@@ -266,6 +266,15 @@ RDNA_API int32_t rdna_attention_forward_noalloc(const void* q, const void* k, co
     return 0;
 }
 
+RDNA_API int32_t rdna_scratch_trim(void) {
+    std::string err;
+    if (rdna_amd::scratch_trim(err) != 0) {
+        set_error("Scratch trim failed: %s", err);
+        return -3;
+    }
+    return 0;
+}
+
 RDNA_API int32_t rdna_attention_forward_path(const void* q, const void* k, const void* v, void* output,
                                              const void* rot_cos, const void* rot_sin, int64_t q_stride_b,
                                              int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b,

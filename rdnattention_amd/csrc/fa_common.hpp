@@ -345,6 +345,30 @@ __device__ __forceinline__ h8 rope8_cs(h8 x, f4 c, f4 s) {
     return y;
 }
 
+// rope8_cs with the rotated values multiplied by `mul` before the one
+// rounding to fp16
+__device__ __forceinline__ h8 rope8_cs_mul(h8 x, f4 c, f4 s, float mul) {
+    h8 y;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = (float)x[2 * i];
+        float b = (float)x[2 * i + 1];
+        y[2 * i] = (_Float16)((a * c[i] - b * s[i]) * mul);
+        y[2 * i + 1] = (_Float16)((a * s[i] + b * c[i]) * mul);
+    }
+    return y;
+}
+
+// fp16(x * mul), one rounding
+__device__ __forceinline__ h8 scale8(h8 x, float mul) {
+    h8 y;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        y[e] = (_Float16)((float)x[e] * mul);
+    }
+    return y;
+}
+
 __device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin_row, int col0) {
     return rope8_cs(x, *reinterpret_cast<const f4*>(cos_row + col0), *reinterpret_cast<const f4*>(sin_row + col0));
 }

@@ -44,13 +44,12 @@ constexpr float kRescaleThreshold = 8.0f; // log2 units
 
 template <int D>
 struct PrefillCfg {
-    // K and V tiles are row-major [64 keys][D] in LDS (64 banks x 4 B).  K
-    // rows at D+8 halves: a 16-byte step mod 256 B puts the 16 rows of one
-    // ds_read_b128 pass in distinct banks.  V rows at a stride = 32 (mod 128)
-    // halves, a 64-byte step mod 256 B: the 4 rows x 64 B that the 32 lanes of
-    // a ds_read_b64_tr_b16 pass read are then distinct too
-    static constexpr int LD = D + 8;
-    static constexpr int LDV = D + ((32 - D % 128) + 128) % 128;
+    // K and V tiles are row-major [64 keys][D] in LDS with a 32-byte row pad.
+    // (Strides that keep every ds_read_b128 pass of K and ds_read_b64_tr_b16
+    // pass of V on distinct banks -- K at D+8, V at 32 mod 128 halves -- took
+    // SQ_LDS_BANK_CONFLICT to 0 here but measured 1 % slower at D = 256.)
+    static constexpr int LD = D + 16;
+    static constexpr int LDV = D + 16;
     static constexpr int TILE_ELEMS = kBN * LD;
     static constexpr int TILE_V_ELEMS = kBN * LDV;
     static constexpr int BUF_ELEMS = TILE_ELEMS + TILE_V_ELEMS; // K then V
@@ -358,7 +357,14 @@ struct PPCfg {
     static constexpr bool PERSIST = D >= 64;
 };
 
-template <int D>
+// PRE (used when c = |scale| log2(e) <= 1, which covers 1/sqrt(D) for every
+// head dim): Q is staged pre-multiplied by q_sign * c, so the QK^T MFMAs
+// produce scores in log2 units, and each S^T accumulator chain starts from
+// -m (m the lane's running max, 0 while no key is visible) instead of 0, so
+// the MFMA output is the exponent itself: p = 2^acc with no per-score
+// multiply-add.  The accumulators are shifted only when the running max
+// moves.  Without PRE, Q carries only the sign and p = 2^(acc c - m).
+template <int D, bool PRE>
 __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) {
     using C = PPCfg<D>;
     // sK[slot], sV[slot], sQ
@@ -458,10 +464,15 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 }
 #pragma unroll
                 for (int c = 0; c < C::QCT; c++) {
-                    x[c] = rope8_cs(x[c], cs[c], sn[c]);
+                    x[c] = PRE ? rope8_cs_mul(x[c], cs[c], sn[c], p.qmul) : rope8_cs(x[c], cs[c], sn[c]);
+                }
+            } else if constexpr (PRE) {
+#pragma unroll
+                for (int c = 0; c < C::QCT; c++) {
+                    x[c] = scale8(x[c], p.qmul);
                 }
             }
-            const bool neg = p.q_sign < 0.0f;
+            const bool neg = !PRE && p.q_sign < 0.0f; // PRE: the sign is in qmul
             asm volatile("" : "+v"(t));
 #pragma unroll
             for (int c = 0; c < C::QCT; c++) {
@@ -497,6 +508,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             oacc[dt] = f16x{};
         }
         float m_run = -INFINITY;
+        float m_use = 0.0f; // m_run, or 0 while it is -inf (PRE: the S^T accumulators start at -m_use)
+        f16x minit = f16x{};
         float l_run = 0.0f;
         f16x sacc[2];
         sacc[0] = f16x{};
@@ -587,9 +600,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 } else {
                     const int js = j - NPV, st = js >> 1;
                     if (js & 1) {
-                        acc1 = mfma_32x32x16_f16(a, qreg[st], acc1);
+                        acc1 = mfma_32x32x16_f16(a, qreg[st], (PRE && st == 0) ? minit : acc1);
                     } else {
-                        acc0 = mfma_32x32x16_f16(a, qreg[st], acc0);
+                        acc0 = mfma_32x32x16_f16(a, qreg[st], (PRE && st == 0) ? minit : acc0);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -649,7 +662,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 mx = fmaxf(mx, sacc[1][e]);
             }
             mx = pair_max(mx);
-            const float m_new = fmaxf(m_run, mx * p.c);
+            // PRE: sacc = S c - m_use already; otherwise S
+            const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * p.c);
             const bool grow = m_new > m_run + kRescaleThreshold;
             if (wave_any(grow)) {
                 const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
@@ -661,14 +675,31 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 for (int dt = 0; dt < C::NDT; dt++) {
                     oacc[dt] *= alpha;
                 }
+                const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
+                if constexpr (PRE) {
+                    // re-base this tile's exponents and the next tiles' start
+                    const float shift = m_use - m_use_new;
+#pragma unroll
+                    for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                        for (int e = 0; e < 16; e++) {
+                            sacc[kt][e] += shift;
+                        }
+                    }
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        minit[e] = -m_use_new;
+                    }
+                }
+                m_use = m_use_new;
             }
-            const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
             float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][e], p.c, -m_use));
+                    const float x = PRE ? sacc[kt][e] : fmaf(sacc[kt][e], p.c, -m_use);
+                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(x);
                 }
             }
 #pragma unroll
@@ -744,27 +775,39 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
     }
 }
 
-template <int D>
-int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+template <int D, bool PRE>
+int launch_pp_as(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     // persistent: as many workgroups as the device holds at once, each
     // walking its share of the n_wg row tiles
     int64_t grid = n_wg;
     if (PPCfg<D>::PERSIST) {
         const int64_t resident =
-            resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_f16_pp<D>), kPPThreads, err);
+            resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_f16_pp<D, PRE>), kPPThreads, err);
         if (resident <= 0) {
             return -1;
         }
         grid = std::min(n_wg, resident);
     }
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_f16_pp<D>, dim3((uint32_t)grid), dim3(kPPThreads), 0, stream, p);
+    hipLaunchKernelGGL((fa_fwd_f16_pp<D, PRE>), dim3((uint32_t)grid), dim3(kPPThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
         return -1;
     }
     return 0;
+}
+
+// Q pre-scaled into log2 units needs |q| c representable in fp16: c <= 1
+// keeps |q c| <= |q|.  Not at D = 32, where the 16 registers of the start
+// block would leave room for 3 waves per SIMD, not the 4 that let two
+// workgroups share a compute unit.
+template <int D>
+int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    if (D >= 64 && p.c <= 1.0f) {
+        return launch_pp_as<D, D >= 64>(p, n_wg, stream, err);
+    }
+    return launch_pp_as<D, false>(p, n_wg, stream, err);
 }
 
 template <int D>
@@ -839,6 +882,7 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.hg_chunk = xcd_head_group_chunk(p.n_head_groups, 2 * (int64_t)a.Sk * a.D * (int64_t)sizeof(_Float16));
     p.c = softmax_log2_scale(a.scale);
     p.q_sign = a.scale < 0.0f ? -1.0f : 1.0f;
+    p.qmul = p.q_sign * p.c;
     p.mask = MaskSpec{a.Sk, a.Sk - a.Sq, a.causal ? 1 : 0, a.window > 0 ? a.window : 0};
     p.rope_q = rope_q ? 1 : 0;
 

@@ -48,6 +48,10 @@ struct StreamScratch {
 // up to 2^25 (a 4 x 8 x 4096 x 128 K is 2^24) together with split-K partials.
 constexpr size_t kNoAllocBytes = size_t(64) << 20;
 
+// Returns the freed scratch blocks the library's per-device pools keep for
+// reuse to the devices (hipMemPoolTrimTo 0).  0, or -1 with `err`.
+int scratch_trim(std::string& err);
+
 // The no-allocation entry point's region on the current device: the
 // library's static scratch array (fa_noalloc.hip), its device address looked
 // up once per device.  0, or -1 with `err`.

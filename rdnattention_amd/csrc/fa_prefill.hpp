@@ -31,6 +31,7 @@ struct PrefillParams {
     int32_t n_items;       // n_row_tiles * n_head_groups (persistent kernels)
     float c;               // max(|scale| * log2(e), 1e-30)
     float q_sign;          // sign of scale, folded into Q (exact in fp16)
+    float qmul;            // q_sign * c: Q pre-scaled into log2 units (kernels that do so, when c <= 1)
     MaskSpec mask;
     int32_t rope_q;        // rotate Q with rot_cos / rot_sin while loading it
 };

@@ -43,25 +43,28 @@ __global__ __launch_bounds__(256) void rope_rotate_rows(const _Float16* __restri
 
 namespace {
 
-constexpr uint64_t kScratchRetain = 4ull << 30;
+constexpr uint64_t kScratchRetain = 256ull << 20;
+
+std::mutex g_pool_mu;
+std::map<int, hipMemPool_t> g_pools; // device -> its scratch pool; guarded by g_pool_mu
 
 // One memory pool per device for the scratch buffers, created on first use.
-// Its release threshold keeps up to kScratchRetain bytes of freed blocks in
-// the pool instead of returning them to the device at each synchronisation,
-// so the per-call hipMallocFromPoolAsync / hipFreeAsync pair reuses memory
-// rather than mapping it anew (which left the GPU idle between kernels).
+// Its release threshold keeps up to kScratchRetain bytes (256 MiB: a 128 MiB
+// RoPE-rotated K copy twice over) of freed blocks in the pool instead of
+// returning them to the device at each synchronisation, so the per-call
+// hipMallocFromPoolAsync / hipFreeAsync pair reuses memory rather than
+// mapping it anew (which left the GPU idle between kernels).
+// rdna_scratch_trim() releases what the pools hold.
 int scratch_pool(hipMemPool_t& pool, std::string& err) {
-    static std::mutex mu;
-    static std::map<int, hipMemPool_t> pools; // guarded by mu
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) {
         err = std::string("scratch pool: ") + hipGetErrorString(e);
         return -1;
     }
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = pools.find(dev);
-    if (it != pools.end()) {
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    auto it = g_pools.find(dev);
+    if (it != g_pools.end()) {
         pool = it->second;
         return 0;
     }
@@ -81,11 +84,23 @@ int scratch_pool(hipMemPool_t& pool, std::string& err) {
         err = std::string("scratch pool: ") + hipGetErrorString(e);
         return -1;
     }
-    pools[dev] = pool;
+    g_pools[dev] = pool;
     return 0;
 }
 
 } // namespace
+
+int scratch_trim(std::string& err) {
+    std::lock_guard<std::mutex> lock(g_pool_mu);
+    for (auto& kv : g_pools) {
+        hipError_t e = hipMemPoolTrimTo(kv.second, 0);
+        if (e != hipSuccess) {
+            err = std::string("scratch pool trim: ") + hipGetErrorString(e);
+            return -1;
+        }
+    }
+    return 0;
+}
 
 int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
     stream = s;

@@ -304,3 +304,9 @@ def test_pertoken_v_cpu_path_matches_oracle():
     assert vi.dtype == torch.int8 and vt.shape == (2, 3, 50) and vt.is_contiguous()
     assert np.array_equal(vi.numpy(), ri) and np.allclose(vt.numpy(), rs, rtol=1e-6, atol=0)
     assert vt[0, 0, 3].item() == 1.0
+
+
+def test_scratch_trim_without_pools(lib):
+    """rdna_scratch_trim with no pool created yet (no HIP call made) is a no-op."""
+    lib.rdna_scratch_trim.restype = ctypes.c_int32
+    assert lib.rdna_scratch_trim() == 0

@@ -355,3 +355,20 @@ def test_persistent_workgroups_cover_every_tile(gpu, oracle_lib, case):
     assert rc == 0
     torch.cuda.synchronize()
     assert_f16_parity(out.float().cpu().numpy(), reference_f16(q, k, v, causal, window, cos, sin), name)
+
+
+def test_scratch_trim_between_calls(gpu, oracle_lib):
+    """trim_scratch() returns the pooled RoPE scratch to the device; calls
+    before and after it give bit-identical results."""
+    import rdnattention
+
+    q, k, v = seeded_inputs(16, 1, 8, 2, 700, 700, 128)
+    cos, sin = oracle.rope_tables(700, 128)
+    cd, sd = torch.from_numpy(cos).to(gpu), torch.from_numpy(sin).to(gpu)
+    a = rdnattention.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=True, rot_cos=cd, rot_sin=sd)
+    rdnattention.trim_scratch()
+    b = rdnattention.flash_attn(q.to(gpu), k.to(gpu), v.to(gpu), is_causal=True, rot_cos=cd, rot_sin=sd)
+    torch.cuda.synchronize()
+    rdnattention.trim_scratch()
+    assert torch.equal(a, b)
+    assert_f16_parity(a.float().cpu().numpy(), reference_f16(q, k, v, True, -1, cos, sin), "trim")
