@@ -380,9 +380,14 @@ __device__ __forceinline__ h8 rope8(h8 x, const float* cos_row, const float* sin
 // costs one memory round trip (with the RoPE loads inside a per-slice branch the compiler
 // waited for each slice's loads in turn); chunks bound the registers the tables hold
 // (a D = 512 row with all its tables live would need 384).
+//
+// With `mul` != 0 the values are multiplied by mul in fp32 before their one
+// rounding to fp16 (and `neg` is ignored: the sign is mul's), the
+// pre-scaling of the kernels whose QK^T yields log2-unit scores.
 template <int NS, int CH = NS>
 __device__ __forceinline__ void load_q_operand(h8 (&out)[NS], const _Float16* qrow, const float* cos_row,
-                                               const float* sin_row, int g, bool valid, bool rope, bool neg) {
+                                               const float* sin_row, int g, bool valid, bool rope, bool neg,
+                                               float mul = 0.0f) {
 #pragma unroll
     for (int s0 = 0; s0 < NS; s0 += CH) {
         constexpr int n = CH; // the last chunk may be partial: slices s0 + s >= NS are skipped
@@ -405,14 +410,21 @@ __device__ __forceinline__ void load_q_operand(h8 (&out)[NS], const _Float16* qr
 #pragma unroll
             for (int s = 0; s < n; s++) {
                 if (s0 + s < NS) {
-                    x[s] = rope8_cs(x[s], c[s], sn[s]);
+                    x[s] = mul != 0.0f ? rope8_cs_mul(x[s], c[s], sn[s], mul) : rope8_cs(x[s], c[s], sn[s]);
+                }
+            }
+        } else if (mul != 0.0f) {
+#pragma unroll
+            for (int s = 0; s < n; s++) {
+                if (s0 + s < NS) {
+                    x[s] = scale8(x[s], mul);
                 }
             }
         }
 #pragma unroll
         for (int s = 0; s < n; s++) {
             if (s0 + s < NS) {
-                out[s0 + s] = valid ? (neg ? -x[s] : x[s]) : h8{};
+                out[s0 + s] = valid ? ((neg && mul == 0.0f) ? -x[s] : x[s]) : h8{};
             }
         }
         // the next chunk's loads are not hoisted above this chunk's rotation

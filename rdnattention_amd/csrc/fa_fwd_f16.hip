@@ -66,18 +66,20 @@ struct PrefillCfg {
 // `prefetch` (staging of the next tiles) is issued right behind the S^T
 // MFMAs so its LDS stores and HBM loads overlap them; the exponentials of the
 // second 32-key half overlap the PV MFMAs of the first.
-template <int D, bool MASKED, class Prefetch>
+// PRE: Q holds q * scale * log2(e) and the S^T chains start at `minit` = -m_use
+// (m_run, or 0 while it is -inf), so the accumulators are the exponents.
+template <int D, bool MASKED, bool PRE, class Prefetch>
 __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const _Float16* __restrict__ sV,
                                           const h8 (&qreg)[PrefillCfg<D>::NS], f16x (&oacc)[PrefillCfg<D>::NDT],
-                                          float& m_run, float& l_run, int klo, int khi, int kt0, float c, int lane,
-                                          Prefetch&& prefetch) {
+                                          float& m_run, float& m_use, f16x& minit, float& l_run, int klo, int khi,
+                                          int kt0, float c, int lane, Prefetch&& prefetch) {
     using C = PrefillCfg<D>;
     const int l32 = lane & 31;
     const int g = lane >> 5;
     f16x sacc[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
-        f16x acc = {};
+        f16x acc = PRE ? minit : f16x{};
 #pragma unroll
         for (int s = 0; s < C::NS; s++) {
             h8 a = *reinterpret_cast<const h8*>(&sK[(kt * 32 + l32) * C::LD + 16 * s + 8 * g]);
@@ -109,7 +111,8 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
         mx = fmaxf(mx, sacc[1][i]);
     }
     mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx * c); // c > 0: -inf stays -inf
+    // c > 0: -inf stays -inf (PRE: sacc = S c - m_use already)
+    const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * c);
     const bool grow = m_new > m_run + kRescaleThreshold;
     if (wave_any(grow)) {
         const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
@@ -121,8 +124,23 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
         for (int dt = 0; dt < C::NDT; dt++) {
             oacc[dt] *= alpha;
         }
+        const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
+        if constexpr (PRE) {
+            const float shift = m_use - m_use_new;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    sacc[kt][i] += shift;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                minit[i] = -m_use_new;
+            }
+        }
+        m_use = m_use_new;
     }
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
 
     // V^T operand rows via transpose reads: lane j of each 16-lane group points
     // at key row 4g + j/4 (+8 for the second half of the slots), columns
@@ -135,7 +153,7 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
         h8 pb[2];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            pb[i >> 3][i & 7] = (_Float16)fast_exp2(fmaf(sacc[kt][i], c, -m_use));
+            pb[i >> 3][i & 7] = (_Float16)fast_exp2(PRE ? sacc[kt][i] : fmaf(sacc[kt][i], c, -m_use));
         }
         psum = sum_h8(pb[1], sum_h8(pb[0], psum));
 #pragma unroll
@@ -154,7 +172,7 @@ __device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const
     l_run += psum;
 }
 
-template <int D>
+template <int D, bool PRE>
 __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_prefill(PrefillParams p) {
     using C = PrefillCfg<D>;
     __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::BUF_ELEMS];
@@ -195,7 +213,7 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         const int qr = valid ? q : 0;
         const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
         load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
-                       p.rope_q != 0, p.q_sign < 0.0f);
+                       p.rope_q != 0, p.q_sign < 0.0f, PRE ? p.qmul : 0.0f);
     }
 
     // ---- key tiles this workgroup can see
@@ -214,6 +232,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         oacc[dt] = f16x{};
     }
     float m_run = -INFINITY;
+    float m_use = 0.0f;
+    f16x minit = f16x{};
     float l_run = 0.0f;
 
     h8 kreg[C::KT];
@@ -290,9 +310,11 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         const _Float16* sK = smem + buf * C::BUF_ELEMS;
         const _Float16* sV = sK + C::TILE_ELEMS;
         if (cls == 1) {
-            tile_step<D, false>(sK, sV, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c, lane, prefetch);
+            tile_step<D, false, PRE>(sK, sV, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0, p.c, lane,
+                                     prefetch);
         } else if (cls == 2) {
-            tile_step<D, true>(sK, sV, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c, lane, prefetch);
+            tile_step<D, true, PRE>(sK, sV, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0, p.c, lane,
+                                    prefetch);
         } else {
             prefetch();
         }
@@ -813,7 +835,11 @@ int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::str
 template <int D>
 int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_f16_prefill<D>, dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
+    if (p.c <= 1.0f) { // Q pre-scaled into log2 units (as launch_pp)
+        hipLaunchKernelGGL((fa_fwd_f16_prefill<D, true>), dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_f16_prefill<D, false>), dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);

@@ -66,10 +66,56 @@ struct WideCfg {
     static_assert(2 * BUF_BYTES <= 160 * 1024, "LDS");
 };
 
-template <int D>
+// Online-softmax bookkeeping shared by the large-head kernels.  PRE: Q holds
+// q * scale * log2(e) and each S^T chain started at minit = -m_use (m_run, or
+// 0 while it is -inf), so the accumulators are already the exponents; a
+// rescale re-bases them and minit.  Returns P^T (fp16) and adds its row sum to
+// l_run.
+template <bool PRE, int NDT>
+__device__ __forceinline__ void wide_softmax(f16x& sacc, f16x (&oacc)[NDT], float& m_run, float& m_use, f16x& minit,
+                                             float& l_run, float c, h8 (&pb)[2]) {
+    float mx = sacc[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) {
+        mx = fmaxf(mx, sacc[i]);
+    }
+    mx = pair_max(mx);
+    const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * c); // c > 0: -inf stays -inf
+    const bool grow = m_new > m_run + kWideRescaleThreshold;
+    if (wave_any(grow)) {
+        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
+        if (grow) {
+            m_run = m_new;
+        }
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            oacc[dt] *= alpha;
+        }
+        const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
+        if constexpr (PRE) {
+            const float shift = m_use - m_use_new;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                sacc[i] += shift;
+                minit[i] = -m_use_new;
+            }
+        }
+        m_use = m_use_new;
+    }
+    float psum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        pb[i >> 3][i & 7] = (_Float16)fast_exp2(PRE ? sacc[i] : fmaf(sacc[i], c, -m_use));
+    }
+    psum = sum_h8(pb[1], sum_h8(pb[0], psum));
+    l_run += psum;
+}
+
+template <int D, bool PRE>
 __device__ __forceinline__ void wide_tile(const char* __restrict__ buf, const h8 (&qreg)[WideCfg<D>::NS],
-                                          f16x (&oacc)[WideCfg<D>::NDT], float& m_run, float& l_run, int row_lo,
-                                          int row_hi, int kt0, float c, int lane) {
+                                          f16x (&oacc)[WideCfg<D>::NDT], float& m_run, float& m_use, f16x& minit,
+                                          float& l_run, int row_lo, int row_hi, int kt0, float c, int lane) {
     using C = WideCfg<D>;
     const int l32 = lane & 31;
     const int g = lane >> 5;
@@ -78,7 +124,7 @@ __device__ __forceinline__ void wide_tile(const char* __restrict__ buf, const h8
 
     // S^T[key][query] over the 32-key tile; K operands stream through a
     // small register ring so the scheduler cannot hoist every LDS read
-    f16x sacc = {};
+    f16x sacc = PRE ? minit : f16x{};
     const _Float16* krow = sK + l32 * C::LDK + 8 * g;
     {
         constexpr int DEPTH = kWideOpDepth < C::NS ? kWideOpDepth : C::NS;
@@ -107,34 +153,8 @@ __device__ __forceinline__ void wide_tile(const char* __restrict__ buf, const h8
             sacc[i] = (off < a || off > b) ? -INFINITY : sacc[i];
         }
     }
-    float mx = sacc[0];
-#pragma unroll
-    for (int i = 1; i < 16; i++) {
-        mx = fmaxf(mx, sacc[i]);
-    }
-    mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx * c); // c > 0: -inf stays -inf
-    const bool grow = m_new > m_run + kWideRescaleThreshold;
-    if (wave_any(grow)) {
-        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
-        if (grow) {
-            m_run = m_new;
-        }
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-            oacc[dt] *= alpha;
-        }
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
     h8 pb[2];
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        pb[i >> 3][i & 7] = (_Float16)fast_exp2(fmaf(sacc[i], c, -m_use));
-    }
-    psum = sum_h8(pb[1], sum_h8(pb[0], psum));
-    l_run += psum;
+    wide_softmax<PRE>(sacc, oacc, m_run, m_use, minit, l_run, c, pb);
 
     // O^T += V^T P^T: pb[u] holds keys 16u + 4g + {0..3, 8..11}; the V^T
     // operand rows come from transpose reads of rows 16u + 8hh + 4g + j16/4
@@ -168,7 +188,7 @@ __device__ __forceinline__ void wide_tile(const char* __restrict__ buf, const h8
     }
 }
 
-template <int D>
+template <int D, bool PRE>
 __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams p) {
     using C = WideCfg<D>;
     __shared__ __attribute__((aligned(16))) char wsm[2 * C::BUF_BYTES];
@@ -208,7 +228,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
         const int qr = valid ? q : 0;
         const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
         load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
-                       p.rope_q != 0, p.q_sign < 0.0f);
+                       p.rope_q != 0, p.q_sign < 0.0f, PRE ? p.qmul : 0.0f);
     }
     // Q is in registers before the first DMA, so the per-tile vmcnt waits
     // below only ever wait for DMAs (the compiler does not see those)
@@ -273,6 +293,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
         oacc[dt] = f16x{};
     }
     float m_run = -INFINITY;
+    float m_use = 0.0f;
+    f16x minit = f16x{};
     float l_run = 0.0f;
 
     if (t_begin < t_end) {
@@ -290,7 +312,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
         const int kt0 = t * kWideBN;
         const int cls = wave_active ? classify_tile(p.mask, q0, q_hi, kt0, kt0 + kWideBN - 1) : 0;
         if (cls != 0) {
-            wide_tile<D>(wsm + slot * C::BUF_BYTES, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c, lane);
+            wide_tile<D, PRE>(wsm + slot * C::BUF_BYTES, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0,
+                              p.c, lane);
         }
     }
     // no DMA may still be writing LDS when the workgroup retires
@@ -347,11 +370,11 @@ struct SplitCfg {
 // One half's share of a 32-key tile.  `xch` is the workgroup's exchange area:
 // [wave][4 chunks][64 lanes][4 floats], so each ds_read/write_b128 pass of 64
 // lanes covers one contiguous 1 KB run.
-template <int D, int C0, int W, class Sync>
+template <int D, int C0, int W, bool PRE, class Sync>
 __device__ __forceinline__ void split_tile(const char* __restrict__ buf, float* __restrict__ xch,
-                                           const h8 (&qreg)[W / 16], f16x (&oacc)[W / 32], float& m_run, float& l_run,
-                                           int row_lo, int row_hi, int kt0, float c, int wave, int lane, bool active,
-                                           Sync&& sync) {
+                                           const h8 (&qreg)[W / 16], f16x (&oacc)[W / 32], float& m_run,
+                                           float& m_use, f16x& minit, float& l_run, int row_lo, int row_hi, int kt0,
+                                           float c, int wave, int lane, bool active, Sync&& sync) {
     using C = SplitCfg<D>;
     constexpr int NS = W / 16;
     constexpr int NDT = W / 32;
@@ -360,7 +383,8 @@ __device__ __forceinline__ void split_tile(const char* __restrict__ buf, float* 
     const _Float16* sK = reinterpret_cast<const _Float16*>(buf);
     const _Float16* sV = reinterpret_cast<const _Float16*>(buf + C::TILE_K_BYTES);
 
-    f16x sacc = {};
+    // PRE: only half 0's partial carries -m_use, so the pair's sum holds it once
+    f16x sacc = (PRE && C0 == 0) ? minit : f16x{};
     if (active) {
         const _Float16* krow = sK + l32 * C::LDK + C0 + 8 * g;
         constexpr int DEPTH = kWideOpDepth < NS ? kWideOpDepth : NS;
@@ -411,34 +435,8 @@ __device__ __forceinline__ void split_tile(const char* __restrict__ buf, float* 
             sacc[i] = (off < a || off > b) ? -INFINITY : sacc[i];
         }
     }
-    float mx = sacc[0];
-#pragma unroll
-    for (int i = 1; i < 16; i++) {
-        mx = fmaxf(mx, sacc[i]);
-    }
-    mx = pair_max(mx);
-    const float m_new = fmaxf(m_run, mx * c); // c > 0: -inf stays -inf
-    const bool grow = m_new > m_run + kWideRescaleThreshold;
-    if (wave_any(grow)) {
-        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
-        if (grow) {
-            m_run = m_new;
-        }
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            oacc[dt] *= alpha;
-        }
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
     h8 pb[2];
-    float psum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        pb[i >> 3][i & 7] = (_Float16)fast_exp2(fmaf(sacc[i], c, -m_use));
-    }
-    psum = sum_h8(pb[1], sum_h8(pb[0], psum));
-    l_run += psum;
+    wide_softmax<PRE>(sacc, oacc, m_run, m_use, minit, l_run, c, pb);
 
     // O^T[C0 + d] += V^T P^T: pb[u] holds keys 16u + 4g + {0..3, 8..11}; the
     // V^T operand rows come from transpose reads of rows 16u + 8hh + 4g + j16/4
@@ -474,7 +472,7 @@ __device__ __forceinline__ void split_tile(const char* __restrict__ buf, float* 
 
 // The work of one half: Q^T operand of its d-range, the key-tile loop, and
 // its output columns.
-template <int D, int C0, int W, class Issue>
+template <int D, int C0, int W, bool PRE, class Issue>
 __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, const _Float16* qbase,
                                            _Float16* obase, int q0, int t_begin, int t_end, int wave, int lane,
                                            Issue&& issue_tile) {
@@ -494,7 +492,8 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
         const bool valid = q < p.Sq;
         const int qr = valid ? q : 0;
         load_q_operand<NS, 8>(qreg, qbase + (int64_t)qr * p.q_ss + C0, p.rot_cos + (int64_t)qr * (D / 2) + C0 / 2,
-                              p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f);
+                              p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f,
+                              PRE ? p.qmul : 0.0f);
     }
     // Q is in registers before the first DMA, so the per-tile vmcnt waits
     // below only ever wait for DMAs (the compiler does not see those)
@@ -508,6 +507,8 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
         oacc[dt] = f16x{};
     }
     float m_run = -INFINITY;
+    float m_use = 0.0f;
+    f16x minit = f16x{};
     float l_run = 0.0f;
 
     if (t_begin < t_end) {
@@ -526,8 +527,8 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
         const int kt0 = t * kWideBN;
         // both halves of a pair have the same rows, so the same class
         const bool cls = active && classify_tile(p.mask, q0, q_hi, kt0, kt0 + kWideBN - 1) != 0;
-        split_tile<D, C0, W>(wsm + slot * C::BUF_BYTES, xch, qreg, oacc, m_run, l_run, row_lo, row_hi, kt0, p.c,
-                             wave, lane, cls, [] { __syncthreads(); });
+        split_tile<D, C0, W, PRE>(wsm + slot * C::BUF_BYTES, xch, qreg, oacc, m_run, m_use, minit, l_run, row_lo,
+                                  row_hi, kt0, p.c, wave, lane, cls, [] { __syncthreads(); });
     }
     // no DMA may still be writing LDS when the workgroup retires
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -551,7 +552,7 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
     }
 }
 
-template <int D>
+template <int D, bool PRE>
 __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wsplit(PrefillParams p) {
     using C = SplitCfg<D>;
     __shared__ __attribute__((aligned(16))) char wsm[2 * C::BUF_BYTES + C::XCH_BYTES];
@@ -623,16 +624,20 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wsplit(PrefillPara
     };
 
     if (half == 0) {
-        split_half<D, 0, C::DA>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
+        split_half<D, 0, C::DA, PRE>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
     } else {
-        split_half<D, C::DA, C::DB>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
+        split_half<D, C::DA, C::DB, PRE>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
     }
 }
 
 template <int D>
 int launch_split_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_f16_wsplit<D>, dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    if (p.c <= 1.0f) { // Q pre-scaled into log2 units (|q c| <= |q| fits fp16)
+        hipLaunchKernelGGL((fa_fwd_f16_wsplit<D, true>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_f16_wsplit<D, false>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -644,7 +649,14 @@ int launch_split_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std
 template <int D>
 int launch_wide_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL(fa_fwd_f16_wide<D>, dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    // Q pre-scaled into log2 units (|q c| <= |q| fits fp16); not at D = 352,
+    // where the 16 registers of the start block would spill
+    constexpr bool kPre = D <= 320;
+    if (kPre && p.c <= 1.0f) {
+        hipLaunchKernelGGL((fa_fwd_f16_wide<D, kPre>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_f16_wide<D, false>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
