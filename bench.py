@@ -92,23 +92,23 @@ class Workload:
 
 WORKLOADS = {
     "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128":
-        Workload("f16", 4, 32, 8, 4096, 4096, 128, True, -1, True, 1, 1.0, "fa_fwd_f16_pp<128>"),
+        Workload("f16", 4, 32, 8, 4096, 4096, 128, True, -1, True, 1, 1.0, "fa_fwd_f16_pp<128, true>"),
     "fp16_mha_b1_h8_s512_d64":
-        Workload("f16", 1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0, "fa_fwd_f16_pp<64>"),
+        Workload("f16", 1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0, "fa_fwd_f16_pp<64, true>"),
     "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128":
-        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128>"),
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, false, false>"),
     "int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128":
-        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, true>", True),
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, true, false>", True),
     "fp16_causal_gqa_b2_h32_kv8_s8192_d128":
-        Workload("f16", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<128>"),
+        Workload("f16", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<128, true>"),
     "fp16_decode_b16_h32_kv8_sq1_sk32768_d128":
         Workload("decode", 16, 32, 8, 1, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
     "fp16_decode_b16_h32_kv8_sq4_sk32768_d128":
         Workload("decode", 16, 32, 8, 4, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
     "fp16_window4096_rope_b1_h16_s16384_d256":
-        Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_prefill<256>"),
+        Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_prefill<256, true>"),
     "fp16_window4096_rope_b1_h16_s4096_d512":
-        Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_wide<512>"),
+        Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_wsplit<512, true>"),
 }
 DEFAULT = "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128"
 SECONDARY = [
@@ -558,14 +558,20 @@ def pmc_derived(directory: str, mean):
                  over the XCDs);
       sclk       GRBM_GUI_ACTIVE / XCDs cycles / mean duration;
       valu/mfma  non-MFMA VALU instructions per MFMA instruction;
-      lds_conflict_per_inst  SQ_LDS_BANK_CONFLICT cycles per LDS instruction."""
-    simds, xcds = 1024, 8
+      lds_conflict_per_inst  SQ_LDS_BANK_CONFLICT cycles per LDS instruction;
+      lds_util   SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE / XCDs x CUs): the share
+                 of cycles each CU's LDS is busy with indexed (ds_*) accesses
+                 (rocprofv3's LdsUtil);
+      wait       SQ_WAIT_ANY / SQ_WAVE_CYCLES: the share of wave time spent
+                 waiting (on memory, LDS, barriers or dependencies)."""
+    simds, xcds, cus = 1024, 8, 256
     for path in Path(directory).rglob("*agent_info.csv"):
         with open(path, newline="") as f:
             for row in csv.DictReader(f):
                 if row.get("Agent_Type") == "GPU" and int(row.get("Simd_Count", 0) or 0) > 0:
                     simds = int(row["Simd_Count"])
                     xcds = max(1, int(row.get("Num_Xcc", 1) or 1))
+                    cus = int(row.get("Cu_Count", cus) or cus)
     dur = {}
     for path in Path(directory).rglob("*kernel_trace.csv"):
         with open(path, newline="") as f:
@@ -594,6 +600,12 @@ def pmc_derived(directory: str, mean):
         conf, lds = c("SQ_LDS_BANK_CONFLICT"), c("SQ_INSTS_LDS")
         if conf is not None and lds:
             items.append(f"lds_conflict_cycles_per_inst={conf / lds:.4f}")
+        idx = c("SQ_LDS_IDX_ACTIVE")
+        if idx is not None and gui:
+            items.append(f"lds_util={idx / (gui * cus):.4f}")
+        wait, wave_cycles = c("SQ_WAIT_ANY"), c("SQ_WAVE_CYCLES")
+        if wait is not None and wave_cycles:
+            items.append(f"wait={wait / wave_cycles:.4f}")
         if items:
             out.append(f"derived {kern[:90]}: " + " ".join(items))
     return out

@@ -85,9 +85,23 @@ def test_profiled_traffic_parses(tmp_path, monkeypatch):
     monkeypatch.setattr(bench, "ROOT", tmp_path)
     assert bench.profiled_traffic(bench.DEFAULT, wl) is None
     (tmp_path / "profiles").mkdir()
-    (tmp_path / "profiles" / f"fa_fwd_f16_pp_128__{bench.DEFAULT}.md").write_text(
+    # rocprofv3's kernel name "fa_fwd_f16_pp<128, true>" -> file-name stem
+    assert wl.kernel == "fa_fwd_f16_pp<128, true>"
+    (tmp_path / "profiles" / f"fa_fwd_f16_pp_128_true__{bench.DEFAULT}.md").write_text(
         "# x\n\ntraffic_bytes_per_launch: 123456\n")
     assert bench.profiled_traffic(bench.DEFAULT, wl) == 123456
+
+
+def test_every_profiled_workload_has_a_summary():
+    """Each bench workload whose traffic is reported reads a committed
+    rocprofv3 summary named after its kernel; a renamed kernel instantiation
+    must come with a renamed summary."""
+    import bench
+
+    for name in [bench.DEFAULT] + bench.SECONDARY:
+        if name == "fp16_mha_b1_h8_s512_d64":
+            continue
+        assert bench.profiled_traffic(name, bench.WORKLOADS[name]) is not None, name
 
 
 def test_pmc_summary(tmp_path, capsys):
@@ -100,6 +114,16 @@ def test_pmc_summary(tmp_path, capsys):
     assert bench.pmc_summary(str(tmp_path)) == 0
     out = capsys.readouterr().out
     assert "FETCH_SIZE" in out and "dispatches=2" in out and "20.0" in out
+
+
+def test_pmc_derived_lds_and_wait(tmp_path):
+    import bench
+
+    mean = {("k", "SQ_LDS_IDX_ACTIVE"): 512.0, ("k", "GRBM_GUI_ACTIVE"): 8 * 4.0,
+            ("k", "SQ_WAIT_ANY"): 30.0, ("k", "SQ_WAVE_CYCLES"): 120.0}
+    (line,) = bench.pmc_derived(str(tmp_path), mean)
+    # 512 LDS-busy cycles over 256 CUs x 4 cycles per XCD; 30 of 120 wave quad-cycles waiting
+    assert "lds_util=0.5000" in line and "wait=0.2500" in line
 
 
 def test_multi_gpu_refused():
