@@ -18,6 +18,8 @@
 
 #include <cstdint>
 
+#include "fa_mask.hpp"
+
 namespace rdna_amd {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -95,86 +97,6 @@ constexpr int waitcnt_lgkm(int n) {
 
 __device__ __forceinline__ bool wave_any(bool pred) {
     return __builtin_amdgcn_ballot_w64(pred) != 0;
-}
-
-// Masking rule of the reference (src/rdna/fa2_forward_f16.hip:325-348 and
-// docs/api.md:150-165), with delta = Sk - Sq:
-//   causal:             key <= q + delta
-//   causal + window w:  q + delta - key < w
-//   window w (no causal): |q + delta - key| <= w / 2
-//   always:             key < Sk
-struct MaskSpec {
-    int32_t sk;
-    int32_t delta;
-    int32_t causal;
-    int32_t window; // > 0 enables; 0 = off
-};
-
-__device__ __forceinline__ bool key_visible(const MaskSpec& m, int q, int key) {
-    bool ok = key < m.sk;
-    int rel = q + m.delta - key;
-    if (m.causal) {
-        ok = ok && rel >= 0;
-    }
-    if (m.window > 0) {
-        if (m.causal) {
-            ok = ok && rel < m.window;
-        } else {
-            int a = rel < 0 ? -rel : rel;
-            ok = ok && a <= (m.window >> 1);
-        }
-    }
-    return ok;
-}
-
-// Inclusive key interval [lo, hi] any row in [q_lo, q_hi] can see.
-// Empty when hi < lo.
-__device__ __forceinline__ void visible_key_range(const MaskSpec& m, int q_lo, int q_hi, int& lo, int& hi) {
-    lo = 0;
-    hi = m.sk - 1;
-    if (m.causal) {
-        hi = min(hi, q_hi + m.delta);
-    }
-    if (m.window > 0) {
-        if (m.causal) {
-            lo = max(lo, q_lo + m.delta - m.window + 1);
-        } else {
-            int hw = m.window >> 1;
-            lo = max(lo, q_lo + m.delta - hw);
-            hi = min(hi, q_hi + m.delta + hw);
-        }
-    }
-}
-
-// Classify a key tile [k_lo, k_hi] against rows [q_lo, q_hi]:
-//   0 = no key visible to any row (skip), 1 = every pair visible (no mask),
-//   2 = mixed (apply the per-element mask).
-__device__ __forceinline__ int classify_tile(const MaskSpec& m, int q_lo, int q_hi, int k_lo, int k_hi) {
-    int lo, hi;
-    visible_key_range(m, q_lo, q_hi, lo, hi);
-    if (hi < lo || k_hi < lo || k_lo > hi) {
-        return 0;
-    }
-    bool full = k_hi < m.sk;
-    if (m.causal) {
-        full = full && (k_hi <= q_lo + m.delta);
-    }
-    if (m.window > 0) {
-        if (m.causal) {
-            full = full && (k_lo > q_hi + m.delta - m.window);
-        } else {
-            int hw = m.window >> 1;
-            full = full && (k_lo >= q_hi + m.delta - hw) && (k_hi <= q_lo + m.delta + hw);
-        }
-    }
-    return full ? 1 : 2;
-}
-
-// Visible keys of one query row q form the interval [lo, hi] (empty when
-// hi < lo).  Same rule as key_visible, evaluated once per row so that masking a
-// tile is two compares per score instead of a branchy predicate.
-__device__ __forceinline__ void row_key_bounds(const MaskSpec& m, int q, int& lo, int& hi) {
-    visible_key_range(m, q, q, lo, hi);
 }
 
 // Workgroup -> (head group, row tile).  The hardware deals workgroups to the

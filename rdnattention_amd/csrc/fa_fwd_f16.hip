@@ -285,6 +285,8 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
         }
     };
 
+    // class of key tile t for this wave's rows (0 skip, 1 no mask, 2 masked)
+    const TileClasses tcls = wave_active ? tile_classes<kBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
     if (t_begin < t_end) {
         load_kv(t_begin);
         store_kv(0);
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_pr
             }
         };
         const int kt0 = t * kBN;
-        const int cls = wave_active ? classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1) : 0;
+        const int cls = tile_class(tcls, t);
         const _Float16* sK = smem + buf * C::BUF_ELEMS;
         const _Float16* sV = sK + C::TILE_ELEMS;
         if (cls == 1) {
@@ -523,6 +525,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
+        // class of key tile t_begin + i for this wave's rows (0 skip, 1 no mask, 2 masked)
+        const TileClasses tcls = wave_active ? tile_classes<kBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
         f16x oacc[C::NDT];
 #pragma unroll
@@ -561,19 +565,19 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 vreg[it] = buffer_load_h8(rv, coff_v[it], 0);
             }
         };
-        // LDS <- registers for pair x
+        // LDS <- registers for pair x.  Written whether or not the tiles exist:
+        // a missing tile was loaded as zeros into a slot that no phase reads
+        // (K(x) for x >= n, V(x - 1) for x < 1 or x > n), and every slot is
+        // written on the same schedule as for an existing tile, after the last
+        // read of its previous contents.  No branches in the VALU phase.
         auto store_pair = [&](int x) {
             _Float16* sK = sKs + (x & 1) * C::TILE_K;
             _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
 #pragma unroll
             for (int it = 0; it < C::CT; it++) {
                 if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
-                    if (x < n) {
-                        *reinterpret_cast<h8*>(&sK[clk[it]]) = kreg[it];
-                    }
-                    if (x >= 1 && x <= n) {
-                        *reinterpret_cast<h8*>(&sV[clv[it]]) = vreg[it];
-                    }
+                    *reinterpret_cast<h8*>(&sK[clk[it]]) = kreg[it];
+                    *reinterpret_cast<h8*>(&sV[clv[it]]) = vreg[it];
                 }
             }
         };
@@ -639,11 +643,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 return;
             }
             const bool do_pv = i >= 1 && cls_prev != 0;
-            int cls_now = 0;
-            if (i < n) {
-                const int kt0 = (t_begin + i) * kBN;
-                cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kBN - 1);
-            }
+            const int cls_now = i < n ? tile_class(tcls, t_begin + i) : 0;
             using T_ = std::true_type;
             using F_ = std::false_type;
             if (do_pv && cls_now != 0) {

@@ -310,6 +310,8 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
             issue_tile(t + 1, slot ^ 1);
         }
         const int kt0 = t * kWideBN;
+        // classified per tile: four more live values (tile_classes) would
+        // spill at D = 352, where this kernel fills 256 VGPRs + 256 AGPRs
         const int cls = wave_active ? classify_tile(p.mask, q0, q_hi, kt0, kt0 + kWideBN - 1) : 0;
         if (cls != 0) {
             wide_tile<D, PRE>(wsm + slot * C::BUF_BYTES, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0,
@@ -510,6 +512,7 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
     float m_use = 0.0f;
     f16x minit = f16x{};
     float l_run = 0.0f;
+    const TileClasses tcls = active ? tile_classes<kWideBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
     if (t_begin < t_end) {
         issue_tile(t_begin, 0);
@@ -526,7 +529,7 @@ __device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, co
         }
         const int kt0 = t * kWideBN;
         // both halves of a pair have the same rows, so the same class
-        const bool cls = active && classify_tile(p.mask, q0, q_hi, kt0, kt0 + kWideBN - 1) != 0;
+        const bool cls = tile_class(tcls, t) != 0;
         split_tile<D, C0, W, PRE>(wsm + slot * C::BUF_BYTES, xch, qreg, oacc, m_run, m_use, minit, l_run, row_lo,
                                   row_hi, kt0, p.c, wave, lane, cls, [] { __syncthreads(); });
     }
