@@ -553,12 +553,20 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         // A tile spans at most kBN rows at a seq stride <= 2^24 elements, so its
         // byte range fits 32 bits (tile_bytes); this keeps the per-tile
         // descriptor set-up to a few scalar instructions.
+        // Each group calls load_pair with x = 0, 1, 2, ... in order, so the tile
+        // addresses advance by one tile stride per call (unsigned arithmetic:
+        // V tile -1 of the first call is never read, its num_records is 0).
+        uint64_t k_addr = reinterpret_cast<uint64_t>(kbase) + (uint64_t)((int64_t)t_begin * kBN * p.k_ss * 2);
+        uint64_t v_addr = reinterpret_cast<uint64_t>(vbase) + (uint64_t)((int64_t)(t_begin - 1) * kBN * p.v_ss * 2);
+        const uint64_t k_step = (uint64_t)(kBN * p.k_ss * 2), v_step = (uint64_t)(kBN * p.v_ss * 2);
         auto load_pair = [&](int x) {
             const int tk = t_begin + x, tv = t_begin + x - 1;
-            const auto rk = make_rsrc(kbase + (int64_t)tk * kBN * p.k_ss,
+            const auto rk = make_rsrc(reinterpret_cast<const void*>(k_addr),
                                       x < n ? tile_bytes<kBN>(Sk - tk * kBN, k_row_b, D * 2) : 0u);
-            const auto rv = make_rsrc(vbase + (int64_t)tv * kBN * p.v_ss,
+            const auto rv = make_rsrc(reinterpret_cast<const void*>(v_addr),
                                       (x >= 1 && x <= n) ? tile_bytes<kBN>(Sk - tv * kBN, v_row_b, D * 2) : 0u);
+            k_addr += k_step;
+            v_addr += v_step;
 #pragma unroll
             for (int it = 0; it < C::CT; it++) {
                 kreg[it] = buffer_load_h8(rk, coff_k[it], 0);
