@@ -1,19 +1,18 @@
-// FP16 FlashAttention-2 forward for gfx950 (MI355X): the prefill kernels for
-// head_dim <= 256 and the FP16 dispatcher.
+// FP16 FlashAttention-2 forward for gfx950 (MI355X): the prefill kernel for
+// head_dim <= 128 and the FP16 dispatcher (D 160..256: fa_fwd_f16_kpair.hip,
+// D 288..512: fa_fwd_f16_wide.hip, decode: fa_fwd_decode.hip).
 //
 // Replaces the reference's forwardKernel / forwardKernelGqa
-// (src/rdna/fa2_forward_f16.hip:633-877) with CDNA4 MFMA designs:
+// (src/rdna/fa2_forward_f16.hip:633-877) with a CDNA4 MFMA design:
 //
 //   * fa_fwd_f16_pp<D> (D <= 128): 8 waves in two groups that alternate an
 //     MFMA phase and a softmax + staging phase (ping-pong, described above
 //     the kernel); persistent grid from D = 64 up; Q staged through LDS with
 //     row-contiguous loads; output stored through LDS as whole rows,
 //     non-temporal
-//   * fa_fwd_f16_prefill<D> (D 160..256): 4 waves, double-buffered K/V tiles,
-//     one barrier per tile
-//   * in both, every wave owns 32 query rows of one head and a workgroup holds
-//     G query heads of one kv head (G | Hq/Hkv, G <= 4), so each K/V tile
-//     staged in LDS serves all of them
+//   * every wave owns 32 query rows of one head and a workgroup holds G query
+//     heads of one kv head (G | Hq/Hkv, G <= 4), so each K/V tile staged in
+//     LDS serves all of them
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_f16: a lane owns one query column,
 //     so the row max/sum are lane-local plus one exchange across half-waves
 //   * P^T leaves the S^T accumulator in exactly the B-operand layout of the
@@ -37,303 +36,9 @@
 namespace rdna_amd {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+constexpr int kWideWorkgroupWaves = 4; // fa_fwd_f16_wide / _wsplit: one wave per SIMD
 constexpr int kBN = 64;                 // keys per tile
 constexpr float kRescaleThreshold = 8.0f; // log2 units
-
-template <int D>
-struct PrefillCfg {
-    // K and V tiles are row-major [64 keys][D] in LDS with a 32-byte row pad.
-    // (Strides that keep every ds_read_b128 pass of K and ds_read_b64_tr_b16
-    // pass of V on distinct banks -- K at D+8, V at 32 mod 128 halves -- took
-    // SQ_LDS_BANK_CONFLICT to 0 here but measured 1 % slower at D = 256.)
-    static constexpr int LD = D + 16;
-    static constexpr int LDV = D + 16;
-    static constexpr int TILE_ELEMS = kBN * LD;
-    static constexpr int TILE_V_ELEMS = kBN * LDV;
-    static constexpr int BUF_ELEMS = TILE_ELEMS + TILE_V_ELEMS; // K then V
-    static constexpr int NS = D / 16;                // QK^T reduction steps
-    static constexpr int NDT = D / 32;               // O^T row tiles
-    static constexpr int KCH = D / 8;                // 16-byte chunks per K/V row
-    static constexpr int TASK = kBN * KCH;
-    static constexpr int KT = (TASK + kThreads - 1) / kThreads;
-    static constexpr int MIN_WG = D <= 128 ? 2 : 1;
-    static constexpr int LDO = D + 8; // output staging rows (halves)
-};
-
-// One 64-key tile for one wave: S^T = K Q^T, online softmax, O^T += V^T P^T.
-// `prefetch` (staging of the next tiles) is issued right behind the S^T
-// MFMAs so its LDS stores and HBM loads overlap them; the exponentials of the
-// second 32-key half overlap the PV MFMAs of the first.
-// PRE: Q holds q * scale * log2(e) and the S^T chains start at `minit` = -m_use
-// (m_run, or 0 while it is -inf), so the accumulators are the exponents.
-template <int D, bool MASKED, bool PRE, class Prefetch>
-__device__ __forceinline__ void tile_step(const _Float16* __restrict__ sK, const _Float16* __restrict__ sV,
-                                          const h8 (&qreg)[PrefillCfg<D>::NS], f16x (&oacc)[PrefillCfg<D>::NDT],
-                                          float& m_run, float& m_use, f16x& minit, float& l_run, int klo, int khi,
-                                          int kt0, float c, int lane, Prefetch&& prefetch) {
-    using C = PrefillCfg<D>;
-    const int l32 = lane & 31;
-    const int g = lane >> 5;
-    f16x sacc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-        f16x acc = PRE ? minit : f16x{};
-#pragma unroll
-        for (int s = 0; s < C::NS; s++) {
-            h8 a = *reinterpret_cast<const h8*>(&sK[(kt * 32 + l32) * C::LD + 16 * s + 8 * g]);
-            acc = mfma_32x32x16_f16(a, qreg[s], acc);
-        }
-        sacc[kt] = acc;
-    }
-    prefetch();
-    if constexpr (MASKED) {
-        // visible iff klo <= key <= khi, key = kt0 + 4g + (compile-time offset)
-        const int a = klo - kt0 - 4 * g;
-        const int b = khi - kt0 - 4 * g;
-#pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int off = kt * 32 + 8 * (i >> 2) + (i & 3);
-                sacc[kt][i] = (off < a || off > b) ? -INFINITY : sacc[kt][i];
-            }
-        }
-    }
-    float mx = sacc[0][0];
-#pragma unroll
-    for (int i = 1; i < 16; i++) {
-        mx = fmaxf(mx, sacc[0][i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        mx = fmaxf(mx, sacc[1][i]);
-    }
-    mx = pair_max(mx);
-    // c > 0: -inf stays -inf (PRE: sacc = S c - m_use already)
-    const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * c);
-    const bool grow = m_new > m_run + kRescaleThreshold;
-    if (wave_any(grow)) {
-        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f; // m_run = -inf -> 0
-        if (grow) {
-            m_run = m_new;
-        }
-        l_run *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; dt++) {
-            oacc[dt] *= alpha;
-        }
-        const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
-        if constexpr (PRE) {
-            const float shift = m_use - m_use_new;
-#pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    sacc[kt][i] += shift;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                minit[i] = -m_use_new;
-            }
-        }
-        m_use = m_use_new;
-    }
-
-    // V^T operand rows via transpose reads: lane j of each 16-lane group points
-    // at key row 4g + j/4 (+8 for the second half of the slots), columns
-    // 16*(lane/16 % 2) + 4*(j % 4) of the 32-column d tile
-    const int j16 = lane & 15;
-    const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LDV + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-    float psum = 0.0f;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++) {
-        h8 pb[2];
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            pb[i >> 3][i & 7] = (_Float16)fast_exp2(PRE ? sacc[kt][i] : fmaf(sacc[kt][i], c, -m_use));
-        }
-        psum = sum_h8(pb[1], sum_h8(pb[0], psum));
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const int u = 2 * kt + hh; // 16-key group: keys 16u + 4g + {0..3, 8..11}
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; dt++) {
-                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                oacc[dt] = mfma_32x32x16_f16(a, pb[hh], oacc[dt]);
-            }
-        }
-    }
-    l_run += psum;
-}
-
-template <int D, bool PRE>
-__global__ __launch_bounds__(kThreads, PrefillCfg<D>::MIN_WG) void fa_fwd_f16_prefill(PrefillParams p) {
-    using C = PrefillCfg<D>;
-    __shared__ __attribute__((aligned(16))) _Float16 smem[2 * C::BUF_ELEMS];
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6;
-    const int lane = tid & 63;
-    const int l32 = lane & 31;
-    const int g = lane >> 5;
-
-    // workgroup -> (head group, row tile); the last (heaviest under a causal
-    // mask) row tiles are issued first, head groups fastest so that
-    // workgroups on one XCD keep sharing the K/V of a kv head
-    const int wg = blockIdx.x;
-    int hg, rt;
-    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
-    const int per_b = p.Hkv * p.groups_per_kv;
-    const int b = hg / per_b;
-    const int rem = hg - b * per_b;
-    const int kvh = rem / p.groups_per_kv;
-    const int sub = rem - kvh * p.groups_per_kv;
-    const int h = kvh * p.ratio + sub * p.G + (wave % p.G);
-    const int wg_q0 = rt * p.rows_per_wg;
-    const int q0 = wg_q0 + (wave / p.G) * 32;
-    const int q = q0 + l32;
-    const bool wave_active = q0 < p.Sq;
-    const int q_hi = min(q0 + 31, p.Sq - 1);
-
-    const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-    const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
-    const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
-    _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
-
-    // ---- Q^T operand, resident in registers: lane holds Q[q][16s + 8g .. +7]
-    h8 qreg[C::NS];
-    {
-        const bool valid = q < p.Sq;
-        const int qr = valid ? q : 0;
-        const _Float16* qrow = qbase + (int64_t)qr * p.q_ss;
-        load_q_operand(qreg, qrow, p.rot_cos + (int64_t)qr * (D / 2), p.rot_sin + (int64_t)qr * (D / 2), g, valid,
-                       p.rope_q != 0, p.q_sign < 0.0f, PRE ? p.qmul : 0.0f);
-    }
-
-    // ---- key tiles this workgroup can see
-    const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
-    int klo, khi;
-    visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
-    int t_begin = 0, t_end = 0;
-    if (khi >= klo) {
-        t_begin = klo / kBN;
-        t_end = khi / kBN + 1;
-    }
-
-    f16x oacc[C::NDT];
-#pragma unroll
-    for (int dt = 0; dt < C::NDT; dt++) {
-        oacc[dt] = f16x{};
-    }
-    float m_run = -INFINITY;
-    float m_use = 0.0f;
-    f16x minit = f16x{};
-    float l_run = 0.0f;
-
-    h8 kreg[C::KT];
-    h8 vreg[C::KT];
-    const int Sk = p.mask.sk;
-    int row_lo, row_hi;
-    row_key_bounds(p.mask, q, row_lo, row_hi);
-
-    // per-thread chunk of a tile: row e / KCH, 16-byte column e % KCH
-    uint32_t koff[C::KT];
-    uint32_t voff[C::KT];
-    int loff[C::KT];  // LDS element offset of the chunk in the K tile, -1 = none
-    int lvoff[C::KT]; // ... in the V tile
-#pragma unroll
-    for (int it = 0; it < C::KT; it++) {
-        const int e = tid + it * kThreads;
-        const bool ok = C::TASK % kThreads == 0 || e < C::TASK;
-        const int row = ok ? e / C::KCH : 0;
-        const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
-        koff[it] = (uint32_t)(((int64_t)row * p.k_ss + 8 * ch) * 2);
-        voff[it] = (uint32_t)(((int64_t)row * p.v_ss + 8 * ch) * 2);
-        loff[it] = ok ? row * C::LD + 8 * ch : -1;
-        lvoff[it] = ok ? row * C::LDV + 8 * ch : -1;
-    }
-
-    // HBM -> registers for tile t.  The buffer resources are rebased to the
-    // tile; rows past Sk fall outside num_records and read as 0.
-    auto load_kv = [&](int t) {
-        const int kt0 = t * kBN;
-        const auto rk = make_rsrc(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kBN>(Sk - kt0, (uint32_t)(p.k_ss * 2), D * 2));
-        const auto rv = make_rsrc(vbase + (int64_t)kt0 * p.v_ss, tile_bytes<kBN>(Sk - kt0, (uint32_t)(p.v_ss * 2), D * 2));
-#pragma unroll
-        for (int it = 0; it < C::KT; it++) {
-            kreg[it] = buffer_load_h8(rk, koff[it], 0);
-            vreg[it] = buffer_load_h8(rv, voff[it], 0);
-        }
-    };
-
-    // registers -> LDS buffer `buf` (K tile, then V tile, both row-major)
-    auto store_kv = [&](int buf) {
-        _Float16* sK = smem + buf * C::BUF_ELEMS;
-        _Float16* sV = sK + C::TILE_ELEMS;
-#pragma unroll
-        for (int it = 0; it < C::KT; it++) {
-            if (C::TASK % kThreads == 0 || loff[it] >= 0) {
-                *reinterpret_cast<h8*>(&sK[loff[it]]) = kreg[it];
-                *reinterpret_cast<h8*>(&sV[lvoff[it]]) = vreg[it];
-            }
-        }
-    };
-
-    // class of key tile t for this wave's rows (0 skip, 1 no mask, 2 masked)
-    const TileClasses tcls = wave_active ? tile_classes<kBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
-    if (t_begin < t_end) {
-        load_kv(t_begin);
-        store_kv(0);
-        if (t_begin + 1 < t_end) {
-            load_kv(t_begin + 1);
-        }
-    }
-    __syncthreads();
-    for (int t = t_begin; t < t_end; t++) {
-        const int buf = (t - t_begin) & 1;
-        // stage tile t+1 into the other buffer (free since the last barrier)
-        // and start loading tile t+2
-        auto prefetch = [&]() {
-            if (t + 1 < t_end) {
-                store_kv(buf ^ 1);
-                if (t + 2 < t_end) {
-                    load_kv(t + 2);
-                }
-            }
-        };
-        const int kt0 = t * kBN;
-        const int cls = tile_class(tcls, t);
-        const _Float16* sK = smem + buf * C::BUF_ELEMS;
-        const _Float16* sV = sK + C::TILE_ELEMS;
-        if (cls == 1) {
-            tile_step<D, false, PRE>(sK, sV, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0, p.c, lane,
-                                     prefetch);
-        } else if (cls == 2) {
-            tile_step<D, true, PRE>(sK, sV, qreg, oacc, m_run, m_use, minit, l_run, row_lo, row_hi, kt0, p.c, lane,
-                                    prefetch);
-        } else {
-            prefetch();
-        }
-        __syncthreads();
-    }
-
-    if (!wave_active) {
-        return;
-    }
-    // ---- normalise once in fp32, round once to fp16; the tile passes through
-    // this wave's part of the K/V buffers, free after the loop's last barrier
-    const float l = pair_sum(l_run);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    static_assert(kWaves * 32 * C::LDO <= 2 * C::BUF_ELEMS, "output staging must fit the K/V buffers");
-    store_o_tile<D, C::LDO>(oacc, [&](int) { return f4{inv, inv, inv, inv}; }, smem + wave * 32 * C::LDO, obase, q0,
-                            p.Sq, p.o_ss, lane);
-}
 
 // ---------------------------------------------------------------------------
 // Ping-pong prefill (D <= 128): 8 waves in two groups that alternate between
@@ -840,22 +545,6 @@ int launch_pp(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::str
     return launch_pp_as<D, false>(p, n_wg, stream, err);
 }
 
-template <int D>
-int launch_prefill(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
-    KernelTimerGuard timer(stream);
-    if (p.c <= 1.0f) { // Q pre-scaled into log2 units (as launch_pp)
-        hipLaunchKernelGGL((fa_fwd_f16_prefill<D, true>), dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL((fa_fwd_f16_prefill<D, false>), dim3((uint32_t)n_wg), dim3(kThreads), 0, stream, p);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        err = hipGetErrorString(e);
-        return -1;
-    }
-    return 0;
-}
-
 } // namespace
 
 constexpr int64_t kMaxSeqStride = 1 << 24;
@@ -902,13 +591,17 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.Hkv = a.Hkv;
     p.ratio = a.Hq / a.Hkv;
     const bool pp = a.D <= 128;
-    if (a.D > kWideSplitMaxPairD) {
+    const bool kpair = a.D > 128 && a.D <= 256;
+    if (kpair) {
+        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
+        p.rows_per_wg = kKPairRows / p.G;
+    } else if (a.D > kWideSplitMaxPairD) {
         // the wave-pair split kernel: two pairs of waves, each pair 32 rows of one head
         p.G = (p.ratio % 2 == 0) ? 2 : 1;
         p.rows_per_wg = 64 / p.G;
     } else {
         p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
-        p.rows_per_wg = 32 * (pp ? kPPWaves : kWaves) / p.G;
+        p.rows_per_wg = 32 * (pp ? kPPWaves : kWideWorkgroupWaves) / p.G;
     }
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
@@ -935,11 +628,10 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     case 64: return launch_pp<64>(p, n_wg, stream, err);
     case 96: return launch_pp<96>(p, n_wg, stream, err);
     case 128: return launch_pp<128>(p, n_wg, stream, err);
-    case 160: return launch_prefill<160>(p, n_wg, stream, err);
-    case 192: return launch_prefill<192>(p, n_wg, stream, err);
-    case 224: return launch_prefill<224>(p, n_wg, stream, err);
-    case 256: return launch_prefill<256>(p, n_wg, stream, err);
     default: break;
+    }
+    if (kpair) {
+        return launch_kpair(p, (int)a.D, n_wg, stream, err);
     }
     if (a.D > 256) {
         return launch_wide(p, (int)a.D, n_wg, stream, err);

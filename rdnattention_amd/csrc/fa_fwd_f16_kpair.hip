@@ -1,0 +1,501 @@
+// FP16 prefill for head_dim 160..256 on gfx950: the two-group ping-pong of
+// the D <= 128 kernel (fa_fwd_f16.hip), with each 32-row tile's work split
+// between a pair of waves so that two waves fit on every SIMD.
+//
+// One wave holding Q^T (D/4 registers per lane) and O^T (D/2) of 32 rows
+// needs 192 registers at D = 256 before any score, operand or staging
+// register, so the one-wave kernel runs one wave per SIMD, its MFMAs and its
+// softmax back to back.  Here waves 2j and 2j+1 (a pair, in the same group)
+// own the same 32 query rows, and half h = wave & 1 of the pair
+//
+//   * computes S^T for keys [32h, 32h + 32) of each 64-key tile, over the
+//     full head dimension (Q^T in registers, D/16 MFMAs);
+//   * accumulates O^T for d in [C0, C0 + W): [0, DA) for half 0, [DA, D) for
+//     half 1, DA = 32 * ceil(D / 64), over all 64 keys (4 W/32 MFMAs).
+//
+// No work is duplicated.  The pair exchanges three things through LDS, each
+// across one of the ping-pong's existing barriers:
+//
+//   M(i): O^T += V(i-1)^T P(i-1)^T, reading the partner's half of P(i-1) and
+//         its row sum; S(i)^T for the own keys; the own tile row max -> LDS
+//   V(i): the pair's max = max(own, partner's), the same in both halves, so
+//         both make the same rescale decisions; P(i) of the own keys -> LDS
+//         together with its row sum; staging of the next K/V tiles
+//
+// The row sum l adds the two halves' sums in one fixed order, so both halves
+// hold the same bits.  Everything else follows fa_fwd_f16_pp: S^T = K Q^T so a
+// lane owns one query column, P^T straight from the S accumulator into the
+// B operand of O^T = V^T P^T, V^T through transpose reads, the lazy max
+// (threshold 2^8), Q pre-scaled into log2 units (PRE), staging through
+// registers with each group storing its 32 rows of every tile, per-row-tile
+// tile classes, and (up to D = 224) a persistent grid.
+#include "fa_common.hpp"
+#include "fa_host.hpp"
+#include "fa_internal.hpp"
+#include "fa_prefill.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+namespace rdna_amd {
+namespace {
+
+constexpr int kKPWaves = 8;
+constexpr int kKPThreads = 64 * kKPWaves;
+constexpr int kKPBN = 64;                  // keys per tile
+constexpr float kKPRescaleThreshold = 8.0f; // log2 units
+
+template <int D>
+struct KPCfg {
+    static_assert(D % 32 == 0 && D >= 160 && D <= 256, "head_dim");
+    // LDS rows (halves): 16-row ds_read_b128 of K at 16-byte steps mod 256 B,
+    // 4-row transpose reads of V at a stride = 32 (mod 128) halves
+    static constexpr int LDK = D + 8;
+    static constexpr int LDV = D + ((32 - D % 128) + 128) % 128;
+    static constexpr int TILE_K = kKPBN * LDK;
+    static constexpr int TILE_V = kKPBN * LDV;
+    static constexpr int NS = D / 16;               // Q K^T reduction steps
+    static constexpr int DA = 32 * ((D + 63) / 64); // O^T columns of half 0
+    static constexpr int DB = D - DA;               // ... of half 1
+    static constexpr int KCH = D / 8;               // 16-byte chunks per K/V row
+    // staging of a group's 32 rows of a K (or V) tile: RPI rows per pass, KCH
+    // threads per row (RPI * KCH <= 256 threads busy), CT passes
+    static constexpr int RPI = 256 / KCH;
+    static constexpr int CT = (32 + RPI - 1) / RPI;
+    // exchange areas: P^T operands [wave][2][64 lanes] of 16 bytes, tile
+    // maxima and row sums [wave][64 lanes] of 4 bytes
+    static constexpr int KV_BYTES = (2 * TILE_K + 2 * TILE_V) * 2;
+    static constexpr int XP_BYTES = kKPWaves * 2 * 64 * 16;
+    static constexpr int XS_BYTES = kKPWaves * 64 * 4;
+    static constexpr int SMEM_BYTES = KV_BYTES + XP_BYTES + 2 * XS_BYTES;
+    // MFMA operands in flight, and a persistent grid: at D = 256 the deeper
+    // ring and the persistent loop's live state do not fit 256 registers
+    static constexpr int OP_DEPTH = D <= 224 ? 4 : 2;
+    static constexpr bool PERSIST = D <= 224;
+    static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
+    static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
+    static_assert(SMEM_BYTES <= 160 * 1024, "LDS");
+};
+
+// The work of one half (C0, W) of every pair, over the persistent grid's
+// row tiles.  Both halves of a group pass the same barriers.
+template <int D, bool PRE, int C0, int W>
+__device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, const int wave) {
+    using C = KPCfg<D>;
+    constexpr int HALF = C0 == 0 ? 0 : 1;
+    constexpr int NDT = W / 32; // O^T row blocks of this half
+    _Float16* const sKs = reinterpret_cast<_Float16*>(smem);
+    _Float16* const sVs = sKs + 2 * C::TILE_K;
+    h8* const xp = reinterpret_cast<h8*>(smem + C::KV_BYTES);
+    float* const xmax = reinterpret_cast<float*>(smem + C::KV_BYTES + C::XP_BYTES);
+    float* const xsum = xmax + kKPWaves * 64;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int pair = wave >> 1;
+    const int partner = wave ^ 1;
+    const int grp = wave >> 2;  // 0 = group A, 1 = group B
+    const int gtid = tid & 255; // thread index inside the group
+
+    // ---- staging: this group's half (rows 32*grp .. +31) of K(x) and V(x-1).
+    // Thread gtid moves chunk ch of rows r0 + RPI*it: one base offset per
+    // thread, the pass's row step as the buffer load's scalar offset and as
+    // the LDS store's immediate offset.
+    const int srow = gtid / C::KCH; // < RPI for the busy threads
+    const int sch = gtid - srow * C::KCH;
+    const bool stager = srow < C::RPI;
+    const int r0 = 32 * grp + (stager ? srow : 0);
+    const uint32_t coff_k = (uint32_t)(((int64_t)r0 * p.k_ss + 8 * sch) * 2);
+    const uint32_t coff_v = (uint32_t)(((int64_t)r0 * p.v_ss + 8 * sch) * 2);
+    const int clk = r0 * C::LDK + 8 * sch;
+    const int clv = r0 * C::LDV + 8 * sch;
+    // pass it moves row r0 + RPI*it, inside the group's 32 rows
+    auto stages = [&](int it) { return stager && (32 % C::RPI == 0 || srow + C::RPI * it < 32); };
+
+    auto run_tile = [&](const int wg) {
+        int hg, rt;
+        wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
+        const int per_b = p.Hkv * p.groups_per_kv;
+        const int b = hg / per_b;
+        const int rem = hg - b * per_b;
+        const int kvh = rem / p.groups_per_kv;
+        const int sub = rem - kvh * p.groups_per_kv;
+        // pair j takes head j % G, rows (j / G) * 32 .. +31 of the row tile
+        const int h = kvh * p.ratio + sub * p.G + (pair % p.G);
+        const int wg_q0 = rt * p.rows_per_wg;
+        const int q0 = wg_q0 + (pair / p.G) * 32;
+        const int q = q0 + l32;
+        const bool wave_active = q0 < p.Sq;
+        const int q_hi = min(q0 + 31, p.Sq - 1);
+
+        const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
+        const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
+
+        const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
+        int klo, khi;
+        visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
+        int t_begin = 0, n = 0;
+        if (khi >= klo) {
+            t_begin = klo / kKPBN;
+            n = khi / kKPBN + 1 - t_begin;
+        }
+        const int Sk = p.mask.sk;
+        const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
+        int row_lo, row_hi;
+        row_key_bounds(p.mask, q, row_lo, row_hi);
+        // class of key tile t_begin + i for this pair's rows (0 skip, 1 no mask,
+        // 2 masked): both halves of a pair share rows, so they share classes
+        const TileClasses tcls = wave_active ? tile_classes<kKPBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
+
+        h8 kreg[C::CT], vreg[C::CT];
+        // Each group calls load_pair with x = 0, 1, 2, ... in order, so the
+        // tile addresses advance by one stride per call (unsigned arithmetic:
+        // V tile -1 of the first call is never read, its num_records is 0).
+        uint64_t k_addr = reinterpret_cast<uint64_t>(kbase) + (uint64_t)((int64_t)t_begin * kKPBN * p.k_ss * 2);
+        uint64_t v_addr = reinterpret_cast<uint64_t>(vbase) + (uint64_t)((int64_t)(t_begin - 1) * kKPBN * p.v_ss * 2);
+        const uint64_t k_step = (uint64_t)(kKPBN * p.k_ss * 2), v_step = (uint64_t)(kKPBN * p.v_ss * 2);
+        auto load_pair = [&](int x) {
+            const int tk = t_begin + x, tv = t_begin + x - 1;
+            const auto rk = make_rsrc(reinterpret_cast<const void*>(k_addr),
+                                      x < n ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
+            const auto rv = make_rsrc(reinterpret_cast<const void*>(v_addr),
+                                      (x >= 1 && x <= n) ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
+            k_addr += k_step;
+            v_addr += v_step;
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                if (stages(it)) {
+                    kreg[it] = buffer_load_h8(rk, coff_k, (uint32_t)(C::RPI * it) * k_row_b);
+                    vreg[it] = buffer_load_h8(rv, coff_v, (uint32_t)(C::RPI * it) * v_row_b);
+                }
+            }
+        };
+        // LDS <- registers for pair x, whether or not the tiles exist: a
+        // missing tile was loaded as zeros into a slot that no phase reads,
+        // written on the same schedule as an existing tile (after the last
+        // read of the slot's previous contents)
+        auto store_pair = [&](int x) {
+            _Float16* sK = sKs + (x & 1) * C::TILE_K;
+            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                if (stages(it)) {
+                    *reinterpret_cast<h8*>(&sK[clk + C::RPI * it * C::LDK]) = kreg[it];
+                    *reinterpret_cast<h8*>(&sV[clv + C::RPI * it * C::LDV]) = vreg[it];
+                }
+            }
+        };
+
+        // the first K/V pair is in flight while Q^T loads (full head dim,
+        // rotated and pre-scaled on the way)
+        if (n > 0) {
+            load_pair(0);
+        }
+        h8 qreg[C::NS];
+        {
+            const bool valid = q < p.Sq;
+            const int qr = valid ? q : 0;
+            const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
+            load_q_operand<C::NS, 2>(qreg, qbase + (int64_t)qr * p.q_ss, p.rot_cos + (int64_t)qr * (D / 2),
+                                     p.rot_sin + (int64_t)qr * (D / 2), g, valid, p.rope_q != 0, p.q_sign < 0.0f,
+                                     PRE ? p.qmul : 0.0f);
+        }
+
+        f16x oacc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            oacc[dt] = f16x{};
+        }
+        float m_run = -INFINITY;
+        float m_use = 0.0f; // m_run, or 0 while it is -inf (PRE: the S^T chain starts at -m_use)
+        f16x minit = f16x{};
+        float l_run = 0.0f;
+        f16x sacc = f16x{};
+        h8 pb[2]; // P^T operands of the own 16-key groups u = 2 HALF, 2 HALF + 1
+        pb[0] = h8{};
+        pb[1] = h8{};
+        float mx_own = -INFINITY; // own tile row max (of S c - m_use with PRE, else of S)
+        float ps_own = 0.0f;      // own row sum of the P held in pb
+        int cls_prev = 0;         // class of the tile whose P is held in pb
+
+        // M(i): O^T += V(i-1)^T P(i-1)^T (i >= 1), then S(i)^T = K(i) Q^T for the
+        // own 32 keys (i < n), as one stream of MFMAs whose LDS operands are read
+        // C::OP_DEPTH MFMAs ahead through a register ring
+        auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+            constexpr bool DO_PV = decltype(do_pv_c)::value;
+            constexpr bool DO_S = decltype(do_s_c)::value;
+            constexpr int NPV = DO_PV ? 4 * NDT : 0; // (u, dt)
+            constexpr int NSK = DO_S ? C::NS : 0;
+            constexpr int T = NPV + NSK;
+            constexpr int DEPTH = T < C::OP_DEPTH ? T : C::OP_DEPTH;
+            const int j16 = lane & 15;
+            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV + C0 +
+                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+            const _Float16* krow = sKs + (i & 1) * C::TILE_K + (32 * HALF + l32) * C::LDK + 8 * g;
+            // the partner's P^T operands (its 16-key groups u = 2 (1 - HALF) + j)
+            h8 pop[2];
+            if constexpr (DO_PV) {
+                pop[0] = xp[(partner * 2 + 0) * 64 + lane];
+                pop[1] = xp[(partner * 2 + 1) * 64 + lane];
+            }
+            auto op = [&](int j) -> h8 {
+                if (j < NPV) {
+                    const int u = j / NDT, dt = j % NDT;
+                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                    h4 lo = lds_read_tr16(base);
+                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+                return *reinterpret_cast<const h8*>(krow + 16 * (j - NPV));
+            };
+            f16x acc = {};
+            h8 ring[DEPTH > 0 ? DEPTH : 1];
+#pragma unroll
+            for (int j = 0; j < DEPTH; j++) {
+                ring[j] = op(j);
+            }
+#pragma unroll
+            for (int j = 0; j < T; j++) {
+                const h8 a = ring[j % DEPTH];
+                if (j + DEPTH < T) {
+                    ring[j % DEPTH] = op(j + DEPTH);
+                }
+                if (j < NPV) {
+                    const int u = j / NDT, dt = j % NDT;
+                    const h8 pu = (u >> 1) == HALF ? pb[u & 1] : pop[u & 1];
+                    oacc[dt] = mfma_32x32x16_f16(a, pu, oacc[dt]);
+                } else {
+                    const int st = j - NPV;
+                    acc = mfma_32x32x16_f16(a, qreg[st], (PRE && st == 0) ? minit : acc);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if constexpr (DO_S) {
+                sacc = acc;
+            }
+        };
+        auto phase_m = [&](int i) {
+            if (!wave_active) {
+                return;
+            }
+            const bool do_pv = i >= 1 && cls_prev != 0;
+            const int cls_now = i < n ? tile_class(tcls, t_begin + i) : 0;
+            if (do_pv) {
+                // the pair's row sum of tile i-1: the same two terms in the same
+                // order in both halves
+                const float po = xsum[partner * 64 + lane];
+                l_run += HALF == 0 ? ps_own + po : po + ps_own;
+            }
+            using T_ = std::true_type;
+            using F_ = std::false_type;
+            if (do_pv && cls_now != 0) {
+                mfma_stream(T_{}, T_{}, i);
+            } else if (do_pv) {
+                mfma_stream(T_{}, F_{}, i);
+            } else if (cls_now != 0) {
+                mfma_stream(F_{}, T_{}, i);
+            }
+            if (cls_now != 0) {
+                if (cls_now == 2) {
+                    // own key e: kt0 + 32 HALF + 8 (e / 4) + 4 g + e % 4
+                    const int kt0 = (t_begin + i) * kKPBN + 32 * HALF;
+                    const int a = row_lo - kt0 - 4 * g;
+                    const int bnd = row_hi - kt0 - 4 * g;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int off = 8 * (e >> 2) + (e & 3);
+                        sacc[e] = (off < a || off > bnd) ? -INFINITY : sacc[e];
+                    }
+                }
+                float mx = sacc[0];
+#pragma unroll
+                for (int e = 1; e < 16; e++) {
+                    mx = fmaxf(mx, sacc[e]);
+                }
+                mx_own = pair_max(mx);
+                xmax[wave * 64 + lane] = mx_own;
+            }
+            cls_prev = cls_now;
+        };
+
+        // V(i): the pair's max, rescale, P of the own keys -> pb and LDS
+        auto phase_v = [&](int i) {
+            (void)i;
+            if (!wave_active || cls_prev == 0) {
+                return;
+            }
+            const float mx = fmaxf(mx_own, xmax[partner * 64 + lane]);
+            // PRE: mx is a max of S c - m_use; otherwise of S
+            const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * p.c);
+            const bool grow = m_new > m_run + kKPRescaleThreshold;
+            if (wave_any(grow)) {
+                const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+                if (grow) {
+                    m_run = m_new;
+                }
+                l_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) {
+                    oacc[dt] *= alpha;
+                }
+                const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
+                if constexpr (PRE) {
+                    const float shift = m_use - m_use_new;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        sacc[e] += shift;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        minit[e] = -m_use_new;
+                    }
+                }
+                m_use = m_use_new;
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float x = PRE ? sacc[e] : fmaf(sacc[e], p.c, -m_use);
+                pb[e >> 3][e & 7] = (_Float16)fast_exp2(x);
+            }
+            ps_own = sum_h8(pb[1], sum_h8(pb[0], 0.0f));
+            xp[(wave * 2 + 0) * 64 + lane] = pb[0];
+            xp[(wave * 2 + 1) * 64 + lane] = pb[1];
+            xsum[wave * 64 + lane] = ps_own;
+        };
+
+        if (n > 0) {
+            store_pair(0);
+            load_pair(1);
+        }
+        __syncthreads();
+        // Both groups pass 2n + 2 barriers after the prologue's; group B
+        // starts one phase late.
+        if (n > 0) {
+            if (grp == 0) {
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 1);
+                    load_pair(i + 2);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+                __syncthreads();
+            } else {
+                store_pair(1);
+                load_pair(2);
+                __syncthreads();
+                for (int i = 0; i < n; i++) {
+                    phase_m(i);
+                    __syncthreads();
+                    store_pair(i + 2);
+                    load_pair(i + 3);
+                    phase_v(i);
+                    __syncthreads();
+                }
+                phase_m(n);
+                __syncthreads();
+            }
+        }
+
+        // O = O^T / l for this half's columns; every LDS read of the row tile
+        // finished before the last barrier, so the next row tile's prologue
+        // may overwrite LDS
+        if (wave_active && q < p.Sq) {
+            const float l = pair_sum(l_run);
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            _Float16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_ss + C0;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
+                             (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
+                    *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
+                }
+            }
+        }
+    };
+    if constexpr (C::PERSIST) {
+        for (int item = 0;; item++) {
+            const int wg = persistent_item(blockIdx.x, gridDim.x, item, p.n_items);
+            if (wg < 0) {
+                break;
+            }
+            run_tile(wg);
+        }
+    } else {
+        run_tile(blockIdx.x);
+    }
+}
+
+template <int D, bool PRE>
+__global__ __launch_bounds__(kKPThreads, 1) void fa_fwd_f16_kpair(PrefillParams p) {
+    using C = KPCfg<D>;
+    __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
+    // The branch between the halves must be wave-uniform (both sides pass
+    // barriers), so its condition is read from the first lane; the wave index
+    // itself stays a vector value (made uniform, everything derived from it
+    // moves to scalar registers and the kernel spills).
+    const int wave = threadIdx.x >> 6;
+    if (__builtin_amdgcn_readfirstlane(wave & 1) == 0) {
+        kpair_half<D, PRE, 0, C::DA>(p, smem, wave);
+    } else {
+        kpair_half<D, PRE, C::DA, C::DB>(p, smem, wave);
+    }
+}
+
+template <int D, bool PRE>
+int launch_kpair_as(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    // persistent: as many workgroups as the device holds at once
+    int64_t grid = n_wg;
+    if (KPCfg<D>::PERSIST) {
+        const int64_t resident =
+            resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_f16_kpair<D, PRE>), kKPThreads, err);
+        if (resident <= 0) {
+            return -1;
+        }
+        grid = std::min(n_wg, resident);
+    }
+    KernelTimerGuard timer(stream);
+    hipLaunchKernelGGL((fa_fwd_f16_kpair<D, PRE>), dim3((uint32_t)grid), dim3(kKPThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        err = hipGetErrorString(e);
+        return -1;
+    }
+    return 0;
+}
+
+template <int D>
+int launch_kpair_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
+    // Q pre-scaled into log2 units when |q| c stays representable (c <= 1);
+    // not above D = 192, where the 16 registers of the accumulator start
+    // would spill inside the key-tile loop
+    constexpr bool kPre = D <= 192;
+    if (kPre && p.c <= 1.0f) {
+        return launch_kpair_as<D, kPre>(p, n_wg, stream, err);
+    }
+    return launch_kpair_as<D, false>(p, n_wg, stream, err);
+}
+
+} // namespace
+
+int launch_kpair(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err) {
+    switch (head_dim) {
+    case 160: return launch_kpair_d<160>(p, n_wg, stream, err);
+    case 192: return launch_kpair_d<192>(p, n_wg, stream, err);
+    case 224: return launch_kpair_d<224>(p, n_wg, stream, err);
+    case 256: return launch_kpair_d<256>(p, n_wg, stream, err);
+    default: break;
+    }
+    err = "unsupported head_dim for the wave-pair prefill kernel";
+    return -1;
+}
+
+} // namespace rdna_amd

@@ -47,4 +47,10 @@ int xcd_head_group_chunk(int n_head_groups, int64_t kv_bytes);
 constexpr int kWideSplitMaxPairD = 352;
 int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
 
+// Prefill for head_dim 160..256 (fa_fwd_f16_kpair.hip): 8 waves, each pair of
+// waves 32 rows of one head, so a workgroup holds kKPairRows / G rows of G
+// heads (the launcher's PrefillParams must be set up that way).
+constexpr int kKPairRows = 128;
+int launch_kpair(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
+
 } // namespace rdna_amd

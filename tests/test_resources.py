@@ -24,7 +24,7 @@ LDS_LIMIT = 160 * 1024
 WAVES_PER_SIMD = {
     "fa_fwd_f16_pp": 2,
     "fa_fwd_int8": 2,
-    "fa_fwd_f16_prefill": 1,
+    "fa_fwd_f16_kpair": 2,
     "fa_fwd_f16_wide": 1,
     "fa_fwd_f16_wsplit": 1,
     "fa_fwd_f16_decode": 1,
@@ -62,7 +62,7 @@ def test_occupancy_fits_the_workgroup(kernels):
         if need is not None:
             assert k["waves_per_simd"] >= need, (k["kernel"], k["waves_per_simd"], need)
             checked += 1
-    # pp 4, prefill 4, wide 3 + wsplit 5, decode 3, int8 4 (+ 2 score-export instantiations)
+    # pp 4, kpair 4, wide 3 + wsplit 5, decode 3, int8 4 (+ 2 score-export instantiations)
     assert checked >= 4 + 4 + 3 + 5 + 3 + 4
 
 
@@ -75,7 +75,7 @@ def test_every_dispatched_head_dim_is_compiled(kernels):
     for d in (32, 64, 96, 128):
         assert has("fa_fwd_f16_pp", d), d
     for d in (160, 192, 224, 256):
-        assert has("fa_fwd_f16_prefill", d), d
+        assert has("fa_fwd_f16_kpair", d), d
     for d in (288, 320, 352):
         assert has("fa_fwd_f16_wide", d), d
     for d in range(384, 513, 32):
