@@ -106,7 +106,7 @@ WORKLOADS = {
     "fp16_decode_b16_h32_kv8_sq4_sk32768_d128":
         Workload("decode", 16, 32, 8, 4, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
     "fp16_window4096_rope_b1_h16_s16384_d256":
-        Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_prefill<256, true>"),
+        Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_kpair<256, false>"),
     "fp16_window4096_rope_b1_h16_s4096_d512":
         Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_wsplit<512, true>"),
 }

@@ -28,7 +28,7 @@
 // B operand of O^T = V^T P^T, V^T through transpose reads, the lazy max
 // (threshold 2^8), Q pre-scaled into log2 units (PRE), staging through
 // registers with each group storing its 32 rows of every tile, per-row-tile
-// tile classes, and (up to D = 224) a persistent grid.
+// tile classes, and (up to D = 192) a persistent grid.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
@@ -66,13 +66,18 @@ struct KPCfg {
     // exchange areas: P^T operands [wave][2][64 lanes] of 16 bytes, tile
     // maxima and row sums [wave][64 lanes] of 4 bytes
     static constexpr int KV_BYTES = (2 * TILE_K + 2 * TILE_V) * 2;
+    // output staging after the key-tile loop, in the K/V area: [pair][32 rows][LDO]
+    static constexpr int LDO = D + 8;
+    static_assert(4 * 32 * LDO <= 2 * TILE_K + 2 * TILE_V, "output staging must fit the K/V area");
+    static_assert(KCH <= 32, "one row per 32 lanes");
     static constexpr int XP_BYTES = kKPWaves * 2 * 64 * 16;
     static constexpr int XS_BYTES = kKPWaves * 64 * 4;
     static constexpr int SMEM_BYTES = KV_BYTES + XP_BYTES + 2 * XS_BYTES;
-    // MFMA operands in flight, and a persistent grid: at D = 256 the deeper
-    // ring and the persistent loop's live state do not fit 256 registers
+    // MFMA operands in flight, and a persistent grid: above D = 192 the
+    // persistent loop's live state, and at D = 256 also the deeper ring, do
+    // not fit 256 registers
     static constexpr int OP_DEPTH = D <= 224 ? 4 : 2;
-    static constexpr bool PERSIST = D <= 224;
+    static constexpr bool PERSIST = D <= 192;
     static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
     static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
     static_assert(SMEM_BYTES <= 160 * 1024, "LDS");
@@ -403,22 +408,47 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             }
         }
 
-        // O = O^T / l for this half's columns; every LDS read of the row tile
-        // finished before the last barrier, so the next row tile's prologue
-        // may overwrite LDS
-        if (wave_active && q < p.Sq) {
+        // O = O^T / l.  Every LDS read of the row tile finished before the last
+        // barrier, so the K/V area is free: each half writes its columns of the
+        // pair's 32 rows into the pair's slot there, and after a barrier each
+        // half stores 16 of those rows whole, 16 bytes per lane, non-temporal
+        // (O is not read again; streaming it past the L2 keeps the K/V tiles
+        // that other row tiles reuse resident).
+        _Float16* const oslot = sKs + pair * 32 * C::LDO;
+        if (wave_active) {
             const float l = pair_sum(l_run);
             const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            _Float16* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)q * p.o_ss + C0;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++) {
                     h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
                              (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
-                    *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
+                    *reinterpret_cast<h4*>(oslot + l32 * C::LDO + C0 + dt * 32 + 8 * qq + 4 * g) = o4;
                 }
             }
+        }
+        __syncthreads(); // both halves' columns are in the slot
+        if (wave_active) {
+            // 32 lanes per row (D/8 <= 32 of them busy), 2 rows per pass; the
+            // indices come from an opaque copy of the lane id so that they are
+            // not hoisted above the key-tile loop
+            int lane_e = lane;
+            asm volatile("" : "+v"(lane_e));
+            const int r0 = 16 * HALF + (lane_e >> 5);
+            const int ch = lane_e & 31;
+            _Float16* const orow0 = p.o + b * p.o_sb + h * p.o_sh + (int64_t)(q0 + r0) * p.o_ss + 8 * ch;
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                const int r = r0 + 2 * c;
+                if (ch < C::KCH && q0 + r < p.Sq) {
+                    const h8 o8 = *reinterpret_cast<const h8*>(oslot + r * C::LDO + 8 * ch);
+                    __builtin_nontemporal_store(o8, reinterpret_cast<h8*>(orow0 + (int64_t)(2 * c) * p.o_ss));
+                }
+            }
+        }
+        if constexpr (C::PERSIST) {
+            __syncthreads(); // the next row tile's prologue writes the K/V area
         }
     };
     if constexpr (C::PERSIST) {
