@@ -37,6 +37,13 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in device code (the host pass
 # warns that it does not know the feature; harmless).
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# FP16 attention kernels: their row maxima (fmaxf over MFMA results and lane
+# exchanges) otherwise get a canonicalising v_max per input that is not known
+# to be a quiet NaN; scores are never NaN there (masked scores are -inf, and
+# every -inf - -inf case is selected away), so the five extra VALU per tile
+# are dropped.  Infinities keep IEEE semantics.  The quantisers keep the
+# default: their amax must treat NaN inputs as torch does.
+NO_NAN_SOURCES = {"fa_fwd_f16.hip", "fa_fwd_f16_kpair.hip"}
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-I{ROOT / 'include'}"]
 
 
@@ -65,7 +72,8 @@ def parse_resource_remarks(text: str, source: str):
 def _compile(src: Path, obj_dir: Path, arch: str, defines, verbose: bool):
     out = obj_dir / (src.name + ".o")
     if src.suffix == ".hip":
-        cmd = [HIPCC, "-x", "hip", f"--offload-arch={arch}", *COMMON, *DEVICE_FLAGS, *defines,
+        extra = ["-fno-honor-nans"] if src.name in NO_NAN_SOURCES else []
+        cmd = [HIPCC, "-x", "hip", f"--offload-arch={arch}", *COMMON, *DEVICE_FLAGS, *extra, *defines,
                "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(out)]
     else:
         cmd = [HIPCC, "-x", "c++", *COMMON, "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", *defines, "-c",
