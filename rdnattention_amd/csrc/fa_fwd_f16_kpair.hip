@@ -45,6 +45,7 @@ constexpr int kKPWaves = 8;
 constexpr int kKPThreads = 64 * kKPWaves;
 constexpr int kKPBN = 64;                  // keys per tile
 constexpr float kKPRescaleThreshold = 8.0f; // log2 units
+constexpr int kKPWalkBlock = 32;           // row tiles that share a key-tile walk start
 
 template <int D>
 struct KPCfg {
@@ -147,29 +148,57 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             t_begin = klo / kKPBN;
             n = khi / kKPBN + 1 - t_begin;
         }
+        // Key-tile walk: step x visits tile T(x) = t_begin + (x + off) mod n.
+        // Under a sliding window the bands of consecutive row tiles start at
+        // increasing tiles, and the workgroups running together on an XCD hold
+        // consecutive row tiles; each starting at its own band start, they
+        // touch that many different tiles per step.  Starting every row tile of
+        // a block of kKPWalkBlock at the block's highest band start (when it lies
+        // inside the own band) makes them walk the same tiles, at most two
+        // distinct ones per step, which then stay in the L2.  Causal bands all
+        // start at tile 0: off = 0.
+        int off = 0;
+        {
+            const int rt_hi = min(rt | (kKPWalkBlock - 1), p.n_row_tiles - 1);
+            const int hi_q0 = rt_hi * p.rows_per_wg;
+            int blo, bhi;
+            visible_key_range(p.mask, hi_q0, min(hi_q0 + p.rows_per_wg, p.Sq) - 1, blo, bhi);
+            const int c = blo / kKPBN;
+            if (bhi >= blo && c > t_begin && c < t_begin + n) {
+                off = c - t_begin;
+            }
+        }
+        auto walk = [&](int x) { // T(x) for 0 <= x < n
+            const int u = x + off;
+            return t_begin + (u >= n ? u - n : u);
+        };
         const int Sk = p.mask.sk;
         const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
-        // class of key tile t_begin + i for this pair's rows (0 skip, 1 no mask,
+        // class of key tile T(i) for this pair's rows (0 skip, 1 no mask,
         // 2 masked): both halves of a pair share rows, so they share classes
         const TileClasses tcls = wave_active ? tile_classes<kKPBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
         h8 kreg[C::CT], vreg[C::CT];
         // Each group calls load_pair with x = 0, 1, 2, ... in order, so the
-        // tile addresses advance by one stride per call (unsigned arithmetic:
-        // V tile -1 of the first call is never read, its num_records is 0).
-        uint64_t k_addr = reinterpret_cast<uint64_t>(kbase) + (uint64_t)((int64_t)t_begin * kKPBN * p.k_ss * 2);
-        uint64_t v_addr = reinterpret_cast<uint64_t>(vbase) + (uint64_t)((int64_t)(t_begin - 1) * kKPBN * p.v_ss * 2);
+        // tile addresses advance by one stride per call and step back n strides
+        // where the walk wraps (unsigned arithmetic: tiles past the walk, and V
+        // tile -1 of the first call, are never read; their num_records is 0).
         const uint64_t k_step = (uint64_t)(kKPBN * p.k_ss * 2), v_step = (uint64_t)(kKPBN * p.v_ss * 2);
+        uint64_t k_addr = reinterpret_cast<uint64_t>(kbase) + (uint64_t)((int64_t)(t_begin + off) * kKPBN * p.k_ss * 2);
+        uint64_t v_addr = reinterpret_cast<uint64_t>(vbase) + (uint64_t)((int64_t)(t_begin + off - 1) * kKPBN * p.v_ss * 2);
         auto load_pair = [&](int x) {
-            const int tk = t_begin + x, tv = t_begin + x - 1;
+            const bool k_ok = x < n, v_ok = x >= 1 && x <= n;
+            const int tk = k_ok ? walk(x) : 0, tv = v_ok ? walk(x - 1) : 0;
             const auto rk = make_rsrc(reinterpret_cast<const void*>(k_addr),
-                                      x < n ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
+                                      k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
             const auto rv = make_rsrc(reinterpret_cast<const void*>(v_addr),
-                                      (x >= 1 && x <= n) ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
-            k_addr += k_step;
-            v_addr += v_step;
+                                      v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
+            // K(x + 1) is tile t_begin after the wrap at x + 1 + off = n;
+            // V(x) likewise after the wrap at x + off = n
+            k_addr += k_step - (x + 1 + off == n ? (uint64_t)n * k_step : 0);
+            v_addr += v_step - (x + off == n ? (uint64_t)n * v_step : 0);
 #pragma unroll
             for (int it = 0; it < C::CT; it++) {
                 if (stages(it)) {
@@ -287,7 +316,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 return;
             }
             const bool do_pv = i >= 1 && cls_prev != 0;
-            const int cls_now = i < n ? tile_class(tcls, t_begin + i) : 0;
+            const int cls_now = i < n ? tile_class(tcls, walk(i)) : 0;
             if (do_pv) {
                 // the pair's row sum of tile i-1: the same two terms in the same
                 // order in both halves
@@ -306,7 +335,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             if (cls_now != 0) {
                 if (cls_now == 2) {
                     // own key e: kt0 + 32 HALF + 8 (e / 4) + 4 g + e % 4
-                    const int kt0 = (t_begin + i) * kKPBN + 32 * HALF;
+                    const int kt0 = walk(i) * kKPBN + 32 * HALF;
                     const int a = row_lo - kt0 - 4 * g;
                     const int bnd = row_hi - kt0 - 4 * g;
 #pragma unroll
