@@ -258,6 +258,30 @@ def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_window{window}")
 
 
+# d, hq, hkv, sq, sk, causal, window: the D 160-256 kernel starts each row
+# tile's key-tile walk at the highest band start of its block of 32 row tiles
+# (when that tile is in its own band) and wraps around; these cover more than
+# one block (row tiles of 128 / G rows), offsets 0 and non-zero in one block, a
+# causal window, Sq != Sk, GQA, and a window wider than the keys
+WALK_CASES = [
+    (160, 2, 2, 4500, 4500, False, 700),
+    (224, 8, 2, 5000, 5000, True, 1000),
+    (256, 3, 3, 3000, 3500, False, 600),
+    (192, 4, 4, 2600, 2600, False, 6000),
+]
+
+
+@pytest.mark.parametrize("case", WALK_CASES, ids=lambda c: f"d{c[0]}_h{c[1]}kv{c[2]}_s{c[3]}x{c[4]}_w{c[6]}")
+def test_pair_kernel_window_walk(gpu, oracle_lib, case):
+    d, hq, hkv, sq, sk, causal, window = case
+    q, k, v = seeded_inputs(11, 1, hq, hkv, sq, sk, d, std=0.5)
+    out = torch.empty_like(q, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal, window) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, causal, window)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"walk_d{d}_w{window}")
+
+
 @pytest.mark.parametrize("d,hq,hkv", [(384, 6, 2), (416, 6, 3), (480, 8, 2), (512, 9, 3), (448, 4, 4)])
 def test_wave_pair_split_gqa(gpu, oracle_lib, d, hq, hkv):
     """The wave-pair split kernel (D > 352) with one head per workgroup (odd
