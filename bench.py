@@ -108,7 +108,7 @@ WORKLOADS = {
     "fp16_window4096_rope_b1_h16_s16384_d256":
         Workload("f16", 1, 16, 16, 16384, 16384, 256, False, 4096, True, 5, 0.5, "fa_fwd_f16_kpair<256, false>"),
     "fp16_window4096_rope_b1_h16_s4096_d512":
-        Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_wsplit<512, true>"),
+        Workload("f16", 1, 16, 16, 4096, 4096, 512, False, 4096, True, 6, 0.5, "fa_fwd_f16_dpair<512>"),
 }
 DEFAULT = "fp16_causal_gqa_rope_b4_h32_kv8_s4096_d128"
 SECONDARY = [

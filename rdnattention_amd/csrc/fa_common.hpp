@@ -229,6 +229,14 @@ __device__ __forceinline__ void dma_load16(i32x4_t rsrc, uint32_t voff, uint32_t
                  : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
                  : "memory", "m0");
 }
+// dma_load16 with a wave-uniform byte offset `soff` (the instruction's scalar
+// offset) added to voff: a loop over rows then keeps one vector offset.
+__device__ __forceinline__ void dma_load16_s(i32x4_t rsrc, uint32_t voff, uint32_t soff, uint32_t lds_byte_addr) {
+    asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_byte_addr)
+                 : "memory", "m0");
+}
 // dma_load16 with the non-temporal cache policy, for bytes read exactly once
 // (split-K decode streams K/V once): they then do not displace lines that are
 // reused. Kernels whose workgroups share K/V through the L2 use dma_load16.

@@ -1,6 +1,7 @@
 // FP16 FlashAttention-2 forward for gfx950 (MI355X): the prefill kernel for
 // head_dim <= 128 and the FP16 dispatcher (D 160..256: fa_fwd_f16_kpair.hip,
-// D 288..512: fa_fwd_f16_wide.hip, decode: fa_fwd_decode.hip).
+// D 288..352: fa_fwd_f16_wide.hip, D 384..512: fa_fwd_f16_dpair.hip, decode:
+// fa_fwd_decode.hip).
 //
 // Replaces the reference's forwardKernel / forwardKernelGqa
 // (src/rdna/fa2_forward_f16.hip:633-877) with a CDNA4 MFMA design:
@@ -36,7 +37,7 @@
 namespace rdna_amd {
 namespace {
 
-constexpr int kWideWorkgroupWaves = 4; // fa_fwd_f16_wide / _wsplit: one wave per SIMD
+constexpr int kWideWorkgroupWaves = 4; // fa_fwd_f16_wide: one wave per SIMD
 constexpr int kBN = 64;                 // keys per tile
 constexpr float kRescaleThreshold = 8.0f; // log2 units
 
@@ -592,13 +593,13 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.ratio = a.Hq / a.Hkv;
     const bool pp = a.D <= 128;
     const bool kpair = a.D > 128 && a.D <= 256;
+    const bool dpair = a.D > kWideMaxD;
     if (kpair) {
         p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
         p.rows_per_wg = kKPairRows / p.G;
-    } else if (a.D > kWideSplitMaxPairD) {
-        // the wave-pair split kernel: two pairs of waves, each pair 32 rows of one head
-        p.G = (p.ratio % 2 == 0) ? 2 : 1;
-        p.rows_per_wg = 64 / p.G;
+    } else if (dpair) {
+        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
+        p.rows_per_wg = kDPairRows / p.G;
     } else {
         p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
         p.rows_per_wg = 32 * (pp ? kPPWaves : kWideWorkgroupWaves) / p.G;
@@ -632,6 +633,9 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     }
     if (kpair) {
         return launch_kpair(p, (int)a.D, n_wg, stream, err);
+    }
+    if (dpair) {
+        return launch_dpair(p, (int)a.D, n_wg, stream, err);
     }
     if (a.D > 256) {
         return launch_wide(p, (int)a.D, n_wg, stream, err);

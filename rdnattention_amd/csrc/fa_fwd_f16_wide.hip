@@ -1,16 +1,18 @@
-// FP16 prefill for large heads (head_dim 288..512, multiples of 32) on gfx950.
+// FP16 prefill for large heads (head_dim 288..352, multiples of 32) on gfx950.
 //
-// Covers the head dims the reference dispatches through its tile planner
+// Covers head dims the reference dispatches through its tile planner
 // (src/rdna/fa2_forward_f16.hip:1045-1066, chooseTile :923-954) with the same
 // results as the smaller-head kernels (fa_fwd_f16.hip); only the data
-// movement changes, because a D = 512 row tile no longer fits the
+// movement changes, because such a row tile no longer fits the
 // register-staged, 64-key design:
 //
-//   * one workgroup = 4 waves (one per SIMD); K and V tiles of 32 keys go
-//     HBM -> LDS with buffer_load ... lds, one DMA instruction per row (D/8
-//     lanes x 16 B), so rows land at a padded stride with no VGPR staging;
-//     LDS is double-buffered and tile t+1 is in flight while tile t is
-//     computed
+//   * one workgroup = 4 waves (one per SIMD); each wave owns 32 query rows of
+//     one head, with Q^T in VGPRs (D/4 per lane) and all D columns of O^T in
+//     the accumulator registers; G heads of one kv head share the workgroup
+//   * K and V tiles of 32 keys go HBM -> LDS with buffer_load ... lds, one DMA
+//     instruction per row (D/8 lanes x 16 B), so rows land at a padded stride
+//     with no VGPR staging; LDS is double-buffered and tile t+1 is in flight
+//     while tile t is computed
 //   * K rows at stride D+8 halves and V rows at a stride = 32 (mod 128)
 //     halves keep the 16-row ds_read_b128 of K and the 4-row transpose reads
 //     of V on distinct banks for every head dim
@@ -19,18 +21,8 @@
 //     one code path for full and boundary tiles (the mask is 16 selects
 //     against 64+ MFMAs per tile)
 //
-// Two layouts by head dim:
-//   * D <= 352 (fa_fwd_f16_wide): each wave owns 32 query rows of one head,
-//     with Q^T in VGPRs (D/4 per lane) and all D columns of O^T in the
-//     accumulator registers; G heads of one kv head share the workgroup
-//   * D > 352 (fa_fwd_f16_wsplit): Q (up to 128 registers) plus O (up to
-//     256) no longer fit one wave, so the two waves of a pair share 32 query
-//     rows and split the head dimension at DA = 32 * ceil(D / 64): each holds
-//     its part of Q and computes a partial S^T over its d-range, the pair adds
-//     the two partials through LDS (in the same order in both waves, so both
-//     hold the same S), both run the same softmax, and each computes the O
-//     columns of its part.  QK^T is computed once (a split into two column
-//     passes that each recompute it costs 1.5x the FLOPs)
+// Head dims 384..512 run fa_fwd_f16_dpair.hip, whose wave pairs split the
+// head dimension so that two waves fit on every SIMD.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
@@ -44,8 +36,6 @@ constexpr int kWideThreads = 64 * kWideWaves;
 constexpr int kWideBN = 32;                   // keys per tile
 constexpr float kWideRescaleThreshold = 8.0f; // log2 units
 constexpr int kWideOpDepth = 4;                // MFMA operands in flight
-
-constexpr int kWideSplitMinD = kWideSplitMaxPairD + 32; // head dims from here on use the wave-pair split
 
 template <int D>
 struct WideCfg {
@@ -340,315 +330,6 @@ __global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wide(PrefillParams
     }
 }
 
-// ---------------------------------------------------------------------------
-// Wave-pair split for D > 352.  Waves 2j and 2j+1 (a pair) own the same 32
-// query rows; half h = wave & 1 owns d-range [C0, C0 + W): h = 0 takes
-// [0, DA), h = 1 takes [DA, D), DA = 32 * ceil(D / 64).  Per 32-key tile:
-//   S_h^T = K[:, C0:C0+W] Q[:, C0:C0+W]^T  (W/16 MFMAs)  -> LDS exchange slot
-//   barrier; S^T = S_0^T + S_1^T in both waves (same order, same bits)
-//   softmax (identical in both waves) -> P^T
-//   O_h^T += V[:, C0:C0+W]^T P^T          (W/32 x 2 MFMAs)
-// Two pairs per workgroup: G (1 or 2) heads of one kv head, 64 / G rows each.
-// ---------------------------------------------------------------------------
-template <int D>
-struct SplitCfg {
-    static_assert(D % 32 == 0 && D >= kWideSplitMinD && D <= 512, "head_dim");
-    static constexpr int DA = 32 * ((D + 63) / 64); // d-range of half 0
-    static constexpr int DB = D - DA;               // d-range of half 1
-    static constexpr int LDK = D + 8;                              // halves
-    static constexpr int LDV = D + ((32 - D % 128) + 128) % 128;   // halves, = 32 (mod 128)
-    static constexpr int TILE_K_BYTES = kWideBN * LDK * 2;
-    static constexpr int TILE_V_BYTES = kWideBN * LDV * 2;
-    static constexpr int BUF_BYTES = TILE_K_BYTES + TILE_V_BYTES;
-    static constexpr int XCH_BYTES = kWideWaves * 64 * 16 * 4;     // one partial S^T per wave
-    static constexpr int KCH = D / 8;                              // 16-byte chunks per row = DMA lanes
-    static constexpr int ROWS_PER_WAVE = kWideBN / kWideWaves;
-    static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
-    static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
-    static_assert(KCH <= 64, "one DMA instruction per row");
-    static_assert(2 * BUF_BYTES + XCH_BYTES <= 160 * 1024, "LDS");
-};
-
-// One half's share of a 32-key tile.  `xch` is the workgroup's exchange area:
-// [wave][4 chunks][64 lanes][4 floats], so each ds_read/write_b128 pass of 64
-// lanes covers one contiguous 1 KB run.
-template <int D, int C0, int W, bool PRE, class Sync>
-__device__ __forceinline__ void split_tile(const char* __restrict__ buf, float* __restrict__ xch,
-                                           const h8 (&qreg)[W / 16], f16x (&oacc)[W / 32], float& m_run,
-                                           float& m_use, f16x& minit, float& l_run, int row_lo, int row_hi, int kt0,
-                                           float c, int wave, int lane, bool active, Sync&& sync) {
-    using C = SplitCfg<D>;
-    constexpr int NS = W / 16;
-    constexpr int NDT = W / 32;
-    const int l32 = lane & 31;
-    const int g = lane >> 5;
-    const _Float16* sK = reinterpret_cast<const _Float16*>(buf);
-    const _Float16* sV = reinterpret_cast<const _Float16*>(buf + C::TILE_K_BYTES);
-
-    // PRE: only half 0's partial carries -m_use, so the pair's sum holds it once
-    f16x sacc = (PRE && C0 == 0) ? minit : f16x{};
-    if (active) {
-        const _Float16* krow = sK + l32 * C::LDK + C0 + 8 * g;
-        constexpr int DEPTH = kWideOpDepth < NS ? kWideOpDepth : NS;
-        h8 ring[DEPTH];
-#pragma unroll
-        for (int j = 0; j < DEPTH; j++) {
-            ring[j] = *reinterpret_cast<const h8*>(krow + 16 * j);
-        }
-#pragma unroll
-        for (int s = 0; s < NS; s++) {
-            const h8 a = ring[s % DEPTH];
-            if (s + DEPTH < NS) {
-                ring[s % DEPTH] = *reinterpret_cast<const h8*>(krow + 16 * (s + DEPTH));
-            }
-            sacc = mfma_32x32x16_f16(a, qreg[s], sacc);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        f4* mine = reinterpret_cast<f4*>(xch + wave * 1024);
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            mine[q4 * 64 + lane] = f4{sacc[4 * q4], sacc[4 * q4 + 1], sacc[4 * q4 + 2], sacc[4 * q4 + 3]};
-        }
-    }
-    sync(); // every wave's partial is in LDS
-    if (!active) {
-        return;
-    }
-    {
-        const f4* other = reinterpret_cast<const f4*>(xch + (wave ^ 1) * 1024);
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const f4 o = other[q4 * 64 + lane];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                // S_0 + S_1 in both halves: the same operands in the same order
-                const float mine_e = sacc[4 * q4 + e];
-                sacc[4 * q4 + e] = C0 == 0 ? mine_e + o[e] : o[e] + mine_e;
-            }
-        }
-    }
-    {
-        // visible iff row_lo <= key <= row_hi, key = kt0 + 4g + off
-        const int a = row_lo - kt0 - 4 * g;
-        const int b = row_hi - kt0 - 4 * g;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int off = 8 * (i >> 2) + (i & 3);
-            sacc[i] = (off < a || off > b) ? -INFINITY : sacc[i];
-        }
-    }
-    h8 pb[2];
-    wide_softmax<PRE>(sacc, oacc, m_run, m_use, minit, l_run, c, pb);
-
-    // O^T[C0 + d] += V^T P^T: pb[u] holds keys 16u + 4g + {0..3, 8..11}; the
-    // V^T operand rows come from transpose reads of rows 16u + 8hh + 4g + j16/4
-    const int j16 = lane & 15;
-    const _Float16* vrow = sV + (4 * g + (j16 >> 2)) * C::LDV + C0 + 16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-    auto vop = [&](int j) -> h8 {
-        const int u = j / NDT, dt = j % NDT;
-        const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-        h4 lo = lds_read_tr16(base);
-        h4 hi = lds_read_tr16(base + 8 * C::LDV);
-        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-    {
-        constexpr int T = 2 * NDT;
-        constexpr int DEPTH = kWideOpDepth < T ? kWideOpDepth : T;
-        h8 ring[DEPTH];
-#pragma unroll
-        for (int j = 0; j < DEPTH; j++) {
-            ring[j] = vop(j);
-        }
-#pragma unroll
-        for (int j = 0; j < T; j++) {
-            const h8 a = ring[j % DEPTH];
-            if (j + DEPTH < T) {
-                ring[j % DEPTH] = vop(j + DEPTH);
-            }
-            const int u = j / NDT, dt = j % NDT;
-            oacc[dt] = mfma_32x32x16_f16(a, pb[u], oacc[dt]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-}
-
-// The work of one half: Q^T operand of its d-range, the key-tile loop, and
-// its output columns.
-template <int D, int C0, int W, bool PRE, class Issue>
-__device__ __forceinline__ void split_half(const PrefillParams& p, char* wsm, const _Float16* qbase,
-                                           _Float16* obase, int q0, int t_begin, int t_end, int wave, int lane,
-                                           Issue&& issue_tile) {
-    using C = SplitCfg<D>;
-    constexpr int NS = W / 16;
-    constexpr int NDT = W / 32;
-    const int l32 = lane & 31;
-    const int g = lane >> 5;
-    const int q = q0 + l32;
-    const bool active = q0 < p.Sq;
-    const int q_hi = min(q0 + 31, p.Sq - 1);
-    float* xch = reinterpret_cast<float*>(wsm + 2 * C::BUF_BYTES);
-
-    // Q^T operand of d-range [C0, C0 + W): lane holds Q[q][C0 + 16s + 8g .. +7]
-    h8 qreg[NS];
-    {
-        const bool valid = q < p.Sq;
-        const int qr = valid ? q : 0;
-        load_q_operand<NS, 8>(qreg, qbase + (int64_t)qr * p.q_ss + C0, p.rot_cos + (int64_t)qr * (D / 2) + C0 / 2,
-                              p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f,
-                              PRE ? p.qmul : 0.0f);
-    }
-    // Q is in registers before the first DMA, so the per-tile vmcnt waits
-    // below only ever wait for DMAs (the compiler does not see those)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-
-    int row_lo, row_hi;
-    row_key_bounds(p.mask, q, row_lo, row_hi);
-    f16x oacc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        oacc[dt] = f16x{};
-    }
-    float m_run = -INFINITY;
-    float m_use = 0.0f;
-    f16x minit = f16x{};
-    float l_run = 0.0f;
-    const TileClasses tcls = active ? tile_classes<kWideBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
-
-    if (t_begin < t_end) {
-        issue_tile(t_begin, 0);
-    }
-    for (int t = t_begin; t < t_end; t++) {
-        const int slot = (t - t_begin) & 1;
-        // this wave's rows of tile t have landed; after the barrier every
-        // wave's have, every wave is done reading tile t-1's slot, and every
-        // wave has read its partner's tile t-1 partial
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-        __syncthreads();
-        if (t + 1 < t_end) {
-            issue_tile(t + 1, slot ^ 1);
-        }
-        const int kt0 = t * kWideBN;
-        // both halves of a pair have the same rows, so the same class
-        const bool cls = tile_class(tcls, t) != 0;
-        split_tile<D, C0, W, PRE>(wsm + slot * C::BUF_BYTES, xch, qreg, oacc, m_run, m_use, minit, l_run, row_lo,
-                                  row_hi, kt0, p.c, wave, lane, cls, [] { __syncthreads(); });
-    }
-    // no DMA may still be writing LDS when the workgroup retires
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-
-    if (!active) {
-        return;
-    }
-    const float l = pair_sum(l_run);
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    if (q < p.Sq) {
-        _Float16* orow = obase + (int64_t)q * p.o_ss + C0;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                h4 o4 = {(_Float16)(oacc[dt][4 * qq + 0] * inv), (_Float16)(oacc[dt][4 * qq + 1] * inv),
-                         (_Float16)(oacc[dt][4 * qq + 2] * inv), (_Float16)(oacc[dt][4 * qq + 3] * inv)};
-                *reinterpret_cast<h4*>(orow + dt * 32 + 8 * qq + 4 * g) = o4;
-            }
-        }
-    }
-}
-
-template <int D, bool PRE>
-__global__ __launch_bounds__(kWideThreads, 1) void fa_fwd_f16_wsplit(PrefillParams p) {
-    using C = SplitCfg<D>;
-    __shared__ __attribute__((aligned(16))) char wsm[2 * C::BUF_BYTES + C::XCH_BYTES];
-
-    const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // wave-uniform
-    const int lane = tid & 63;
-    const int pair = wave >> 1;
-    const int half = wave & 1;
-
-    // workgroup -> (head group, row tile), as in the other prefill kernels;
-    // pair j takes head j % G, rows (j / G) * 32 .. +31 of the row tile
-    const int wg = blockIdx.x;
-    int hg, rt;
-    wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
-    const int per_b = p.Hkv * p.groups_per_kv;
-    const int b = hg / per_b;
-    const int rem = hg - b * per_b;
-    const int kvh = rem / p.groups_per_kv;
-    const int sub = rem - kvh * p.groups_per_kv;
-    const int h = kvh * p.ratio + sub * p.G + (pair % p.G);
-    const int wg_q0 = rt * p.rows_per_wg;
-    const int q0 = wg_q0 + (pair / p.G) * 32;
-
-    const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-    const _Float16* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
-    const _Float16* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
-    _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
-
-    const int wg_q_hi = min(wg_q0 + p.rows_per_wg, p.Sq) - 1;
-    int klo, khi;
-    visible_key_range(p.mask, wg_q0, wg_q_hi, klo, khi);
-    int t_begin = 0, t_end = 0;
-    if (khi >= klo) {
-        t_begin = klo / kWideBN;
-        t_end = khi / kWideBN + 1;
-    }
-
-    // this wave's DMA rows of every tile: K and V rows wave*8 .. wave*8+7,
-    // lane i moving bytes 16i .. 16i+15 of the row (i < D/8)
-    const int r0 = wave * C::ROWS_PER_WAVE;
-    const uint32_t lane_b = 16u * (uint32_t)lane;
-    const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
-    const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
-    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(wsm);
-    auto issue_tile = [&](int t, int slot) {
-        const int kt0 = t * kWideBN;
-        const int sk_left = p.mask.sk - kt0;
-        auto uniform = [](i32x4_t r) {
-            for (int e = 0; e < 4; e++) {
-                r[e] = __builtin_amdgcn_readfirstlane(r[e]);
-            }
-            return r;
-        };
-        const i32x4_t rk =
-            uniform(make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kWideBN>(sk_left, k_row_b, D * 2)));
-        const i32x4_t rv =
-            uniform(make_rsrc_v(vbase + (int64_t)kt0 * p.v_ss, tile_bytes<kWideBN>(sk_left, v_row_b, D * 2)));
-        const uint32_t sk = lds0 + slot * C::BUF_BYTES;
-        const uint32_t sv = sk + C::TILE_K_BYTES;
-        if (lane < C::KCH) {
-#pragma unroll
-            for (int j = 0; j < C::ROWS_PER_WAVE; j++) {
-                const int r = r0 + j;
-                dma_load16(rk, lane_b + (uint32_t)r * k_row_b, __builtin_amdgcn_readfirstlane(sk + r * (C::LDK * 2)));
-                dma_load16(rv, lane_b + (uint32_t)r * v_row_b, __builtin_amdgcn_readfirstlane(sv + r * (C::LDV * 2)));
-            }
-        }
-    };
-
-    if (half == 0) {
-        split_half<D, 0, C::DA, PRE>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
-    } else {
-        split_half<D, C::DA, C::DB, PRE>(p, wsm, qbase, obase, q0, t_begin, t_end, wave, lane, issue_tile);
-    }
-}
-
-template <int D>
-int launch_split_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
-    KernelTimerGuard timer(stream);
-    if (p.c <= 1.0f) { // Q pre-scaled into log2 units (|q c| <= |q| fits fp16)
-        hipLaunchKernelGGL((fa_fwd_f16_wsplit<D, true>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
-    } else {
-        hipLaunchKernelGGL((fa_fwd_f16_wsplit<D, false>), dim3((uint32_t)n_wg), dim3(kWideThreads), 0, stream, p);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) {
-        err = hipGetErrorString(e);
-        return -1;
-    }
-    return 0;
-}
-
 template <int D>
 int launch_wide_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     KernelTimerGuard timer(stream);
@@ -671,19 +352,14 @@ int launch_wide_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std:
 } // namespace
 
 int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err) {
-    static_assert(kWideSplitMinD == 384, "the switch below dispatches 384.. to the split kernel");
+    static_assert(kWideMaxD == 352, "the switch below covers 288..kWideMaxD");
     switch (head_dim) {
     case 288: return launch_wide_d<288>(p, n_wg, stream, err);
     case 320: return launch_wide_d<320>(p, n_wg, stream, err);
     case 352: return launch_wide_d<352>(p, n_wg, stream, err);
-    case 384: return launch_split_d<384>(p, n_wg, stream, err);
-    case 416: return launch_split_d<416>(p, n_wg, stream, err);
-    case 448: return launch_split_d<448>(p, n_wg, stream, err);
-    case 480: return launch_split_d<480>(p, n_wg, stream, err);
-    case 512: return launch_split_d<512>(p, n_wg, stream, err);
     default: break;
     }
-    err = "unsupported head_dim (multiples of 32 from 32 to 512)";
+    err = "unsupported head_dim for the large-head prefill kernel";
     return -1;
 }
 

@@ -243,11 +243,24 @@ def test_empty_key_sequence_outputs_zero(gpu):
     assert torch.count_nonzero(out) == 0
 
 
+@pytest.mark.parametrize("d,sq,sk", [(512, 70, 20), (384, 40, 32), (448, 33, 33), (480, 130, 64), (512, 200, 45)])
+def test_pair_kernel_few_key_tiles(gpu, oracle_lib, d, sq, sk):
+    """The D 384-512 kernel with one or two 32-key tiles (its prologue DMAs
+    one or two tile pairs, and the first in-loop DMA issue is skipped), full
+    and partial tiles, causal with Sq != Sk."""
+    q, k, v = seeded_inputs(17, 1, 4, 2, sq, sk, d)
+    out = torch.full_like(q, float("nan"), device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, True, -1) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, True, -1)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"few_tiles d{d} {sq}x{sk}")
+
+
 @pytest.mark.parametrize("d,s,window", [(256, 2048, 1024), (512, 1024, 1024), (416, 640, 256)])
 def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     """The large-head window workloads (two-sided window, RoPE, N(0, 0.5)) at
-    a size the oracle finishes quickly; D = 416 runs the wave-pair split with
-    unequal halves (224 + 192 of the head dimension)."""
+    a size the oracle finishes quickly; D = 416 runs the head-dimension pair
+    kernel with unequal halves (224 + 192 of the head dimension)."""
     q, k, v = seeded_inputs(4, 1, 2, 2, s, s, d, std=0.5)
     cos, sin = oracle.rope_tables(s, d)
     out = torch.empty_like(q, device=gpu)
@@ -258,16 +271,19 @@ def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     assert_f16_parity(out.float().cpu().numpy(), ref, f"d{d}_window{window}")
 
 
-# d, hq, hkv, sq, sk, causal, window: the D 160-256 kernel starts each row
-# tile's key-tile walk at the highest band start of its block of 32 row tiles
-# (when that tile is in its own band) and wraps around; these cover more than
-# one block (row tiles of 128 / G rows), offsets 0 and non-zero in one block, a
-# causal window, Sq != Sk, GQA, and a window wider than the keys
+# d, hq, hkv, sq, sk, causal, window: the D 160-256 and D 384-512 pair
+# kernels start each row tile's key-tile walk at the highest band start of its
+# block of 32 row tiles (when that tile is in its own band) and wrap around;
+# these cover more than one block (row tiles of 128 / G rows), offsets 0 and
+# non-zero in one block, a causal window, Sq != Sk, GQA, and a window wider
+# than the keys
 WALK_CASES = [
     (160, 2, 2, 4500, 4500, False, 700),
     (224, 8, 2, 5000, 5000, True, 1000),
     (256, 3, 3, 3000, 3500, False, 600),
     (192, 4, 4, 2600, 2600, False, 6000),
+    (512, 2, 2, 4500, 4500, False, 700),
+    (416, 4, 2, 4200, 4400, True, 900),
 ]
 
 
@@ -284,9 +300,10 @@ def test_pair_kernel_window_walk(gpu, oracle_lib, case):
 
 @pytest.mark.parametrize("d,hq,hkv", [(384, 6, 2), (416, 6, 3), (480, 8, 2), (512, 9, 3), (448, 4, 4)])
 def test_wave_pair_split_gqa(gpu, oracle_lib, d, hq, hkv):
-    """The wave-pair split kernel (D > 352) with one head per workgroup (odd
-    GQA ratios and MHA) and two (even ratios), causal with RoPE, ragged row
-    and key counts, equal and unequal halves of the head dimension."""
+    """The head-dimension pair kernel (D > 352) with one head per workgroup
+    (odd GQA ratios and MHA), two (ratio 2 mod 4) and four (ratios divisible
+    by 4), causal with RoPE, ragged row and key counts, equal and unequal
+    halves of the head dimension."""
     log(f"[split] d{d} hq{hq} hkv{hkv}")
     q, k, v = seeded_inputs(15, 2, hq, hkv, 150, 213, d)
     cos, sin = oracle.rope_tables(213, d)
