@@ -1,7 +1,6 @@
 // FP16 FlashAttention-2 forward for gfx950 (MI355X): the prefill kernel for
 // head_dim <= 128 and the FP16 dispatcher (D 160..256: fa_fwd_f16_kpair.hip,
-// D 288..352: fa_fwd_f16_wide.hip, D 384..512: fa_fwd_f16_dpair.hip, decode:
-// fa_fwd_decode.hip).
+// D 288..512: fa_fwd_f16_dpair.hip, decode: fa_fwd_decode.hip).
 //
 // Replaces the reference's forwardKernel / forwardKernelGqa
 // (src/rdna/fa2_forward_f16.hip:633-877) with a CDNA4 MFMA design:
@@ -37,7 +36,6 @@
 namespace rdna_amd {
 namespace {
 
-constexpr int kWideWorkgroupWaves = 4; // fa_fwd_f16_wide: one wave per SIMD
 constexpr int kBN = 64;                 // keys per tile
 constexpr float kRescaleThreshold = 8.0f; // log2 units
 
@@ -591,19 +589,13 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     p.Sq = a.Sq;
     p.Hkv = a.Hkv;
     p.ratio = a.Hq / a.Hkv;
-    const bool pp = a.D <= 128;
     const bool kpair = a.D > 128 && a.D <= 256;
-    const bool dpair = a.D > kWideMaxD;
-    if (kpair) {
-        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
-        p.rows_per_wg = kKPairRows / p.G;
-    } else if (dpair) {
-        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
-        p.rows_per_wg = kDPairRows / p.G;
-    } else {
-        p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
-        p.rows_per_wg = 32 * (pp ? kPPWaves : kWideWorkgroupWaves) / p.G;
-    }
+    const bool dpair = a.D > 256;
+    // every kernel holds G query heads of one kv head (G | Hq/Hkv, G <= 4)
+    // and 128 (query, head) rows per workgroup: 8 waves of 32 rows (D <= 128)
+    // or 4 pairs of waves of 32 rows (D > 128)
+    p.G = (p.ratio % 4 == 0) ? 4 : ((p.ratio % 2 == 0) ? 2 : 1);
+    p.rows_per_wg = (kpair ? kKPairRows : dpair ? kDPairRows : 32 * kPPWaves) / p.G;
     p.n_row_tiles = (a.Sq + p.rows_per_wg - 1) / p.rows_per_wg;
     p.groups_per_kv = p.ratio / p.G;
     p.n_head_groups = a.B * a.Hkv * p.groups_per_kv;
@@ -636,9 +628,6 @@ int fwd_f16_prefill(const AttnArgs& a, bool rope_q, hipStream_t stream, std::str
     }
     if (dpair) {
         return launch_dpair(p, (int)a.D, n_wg, stream, err);
-    }
-    if (a.D > 256) {
-        return launch_wide(p, (int)a.D, n_wg, stream, err);
     }
     err = "unsupported head_dim (multiples of 32 from 32 to 512)";
     return -1;

@@ -1,17 +1,17 @@
-// FP16 prefill for head_dim 384..512 on gfx950: the two-group ping-pong of
+// FP16 prefill for head_dim 288..512 on gfx950: the two-group ping-pong of
 // the smaller-head kernels (fa_fwd_f16.hip, fa_fwd_f16_kpair.hip), with the
 // head dimension of each 32-row tile split between a pair of waves so that two
 // waves fit on every SIMD.
 //
 // One wave holding Q^T (D/4 registers per lane) and O^T (D/2) of 32 rows
-// needs 384 registers at D = 512, so a one-wave-per-row-tile kernel runs one
-// wave per SIMD with its MFMAs and its softmax back to back.  Here waves 2j
+// needs 216 (D = 288) to 384 (D = 512) registers, so a one-wave-per-row-tile
+// kernel runs one wave per SIMD with its MFMAs and its softmax back to back.  Here waves 2j
 // and 2j+1 (a pair, in the same group) own the same 32 query rows, and half
 // h = wave & 1 owns the head-dimension range [C0, C0 + W): [0, DA) for half
 // 0, [DA, D) for half 1, DA = 32 * ceil(D / 64).  Per 32-key tile each half
 // computes the partial S_h^T = K[:, C0:C0+W] Q[:, C0:C0+W]^T (W/16 MFMAs) and
 // O_h^T += V[:, C0:C0+W]^T P^T (W/16 MFMAs): 32 MFMAs per phase at D = 512,
-// as in the D <= 128 kernel.
+// as in the D <= 128 kernel, 20 at D = 288.
 //
 // The softmax runs once per pair, in half 0; the pair talks through a small
 // per-pair LDS area, across the ping-pong's existing barriers:
@@ -50,11 +50,10 @@ constexpr int kDPThreads = 64 * kDPWaves;
 constexpr int kDPBN = 32;                  // keys per tile
 constexpr float kDPRescaleThreshold = 8.0f; // log2 units
 constexpr int kDPWalkBlock = 32;           // row tiles that share a key-tile walk start
-constexpr int kDPOpDepth = 2;              // MFMA operands in flight
 
 template <int D>
 struct DPCfg {
-    static_assert(D % 32 == 0 && D >= 384 && D <= 512, "head_dim");
+    static_assert(D % 32 == 0 && D >= 288 && D <= 512, "head_dim");
     static constexpr int DA = 32 * ((D + 63) / 64); // head-dim range of half 0
     static constexpr int DB = D - DA;               // ... of half 1
     static constexpr int LDK = D + 8;                              // halves
@@ -70,6 +69,9 @@ struct DPCfg {
     static constexpr int SMEM_BYTES = KV_BYTES + (kDPWaves / 2) * XPAIR_BYTES;
     // rows of each K and V tile one DMA-issuing wave moves (two such waves)
     static constexpr int DMA_ROWS = kDPBN / 2;
+    // MFMA operands in flight: a deeper ring gains 0.3-2 % where it fits the
+    // 256 registers, up to D = 448
+    static constexpr int OP_DEPTH = D <= 448 ? 4 : 2;
     static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
     static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
     static_assert(KCH <= 64, "one DMA instruction per row");
@@ -78,7 +80,7 @@ struct DPCfg {
 
 // The work of one half (C0, W) of every pair over one row tile.  Both
 // halves of a group pass the same barriers.
-template <int D, int C0, int W>
+template <int D, bool PRE, int C0, int W>
 __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, const int wave) {
     using C = DPCfg<D>;
     constexpr int HALF = C0 == 0 ? 0 : 1;
@@ -201,7 +203,8 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
         const int qr = valid ? q : 0;
         const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
         load_q_operand<NS, 2>(qreg, qbase + (int64_t)qr * p.q_ss + C0, p.rot_cos + (int64_t)qr * (D / 2) + C0 / 2,
-                              p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f);
+                              p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f,
+                              PRE ? p.qmul : 0.0f);
     }
     // Q is in registers before the first DMA, so the vmcnt waits below only
     // ever wait for DMAs (which the compiler does not track)
@@ -214,6 +217,7 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
     }
     float m_run = -INFINITY; // half 0 only
     float m_use = 0.0f;      // m_run, or 0 while it is -inf
+    f16x minit = f16x{};     // PRE, half 0: the S^T chain starts at -m_use
     float l_run = 0.0f;
     f16x sacc = f16x{};
     h8 pb[2]; // half 0: P^T of the tile whose PV is pending
@@ -223,14 +227,14 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
 
     // M(i): S_h(i)^T = K(i) Q^T over this half's d-range (i < n), then
     // O_h^T += V(i-1)^T P(i-1)^T (i >= 1), as one stream of MFMAs whose LDS
-    // operands are read kDPOpDepth MFMAs ahead through a register ring
+    // operands are read C::OP_DEPTH MFMAs ahead through a register ring
     auto mfma_stream = [&](auto do_s_c, auto do_pv_c, int i) {
         constexpr bool DO_S = decltype(do_s_c)::value;
         constexpr bool DO_PV = decltype(do_pv_c)::value;
         constexpr int NSK = DO_S ? NS : 0;
         constexpr int NPV = DO_PV ? 2 * NDT : 0; // (u, dt)
         constexpr int T = NSK + NPV;
-        constexpr int DEPTH = T < kDPOpDepth ? T : kDPOpDepth;
+        constexpr int DEPTH = T < C::OP_DEPTH ? T : C::OP_DEPTH;
         const int j16 = lane & 15;
         const _Float16* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + C0 + 8 * g;
         const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV + C0 +
@@ -278,7 +282,8 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
                 }
             }
             if (j < NSK) {
-                acc = mfma_32x32x16_f16(a, qreg[j], acc);
+                // PRE: only half 0's chain starts at -m_use, so the pair's sum holds it once
+                acc = mfma_32x32x16_f16(a, qreg[j], (PRE && HALF == 0 && j == 0) ? minit : acc);
             } else {
                 const int jv = j - NSK, u = jv / NDT, dt = jv % NDT;
                 oacc[dt] = mfma_32x32x16_f16(a, HALF == 0 ? pb[u] : pop[u], oacc[dt]);
@@ -345,7 +350,8 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
                 mx = fmaxf(mx, sacc[e]);
             }
             mx = pair_max(mx);
-            const float m_new = fmaxf(m_run, mx * p.c); // c > 0: -inf stays -inf
+            // PRE: mx is a max of S c - m_use; otherwise of S (c > 0: -inf stays -inf)
+            const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * p.c);
             const bool grow = m_new > m_run + kDPRescaleThreshold;
             float alpha = 1.0f;
             if (wave_any(grow)) {
@@ -358,11 +364,21 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
                 for (int dt = 0; dt < NDT; dt++) {
                     oacc[dt] *= alpha;
                 }
-                m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+                const float m_use_new = (m_run == -INFINITY) ? 0.0f : m_run;
+                if constexpr (PRE) {
+                    // re-base this tile's exponents and the next tiles' start
+                    const float shift = m_use - m_use_new;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        sacc[e] += shift;
+                        minit[e] = -m_use_new;
+                    }
+                }
+                m_use = m_use_new;
             }
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                pb[e >> 3][e & 7] = (_Float16)fast_exp2(fmaf(sacc[e], p.c, -m_use));
+                pb[e >> 3][e & 7] = (_Float16)fast_exp2(PRE ? sacc[e] : fmaf(sacc[e], p.c, -m_use));
             }
             l_run = sum_h8(pb[1], sum_h8(pb[0], l_run));
             xp[lane] = pb[0];
@@ -449,7 +465,7 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
     }
 }
 
-template <int D>
+template <int D, bool PRE>
 __global__ __launch_bounds__(kDPThreads, 1) void fa_fwd_f16_dpair(PrefillParams p) {
     using C = DPCfg<D>;
     __shared__ __attribute__((aligned(16))) char smem[C::SMEM_BYTES];
@@ -458,16 +474,24 @@ __global__ __launch_bounds__(kDPThreads, 1) void fa_fwd_f16_dpair(PrefillParams 
     // itself stays a vector value.
     const int wave = threadIdx.x >> 6;
     if (__builtin_amdgcn_readfirstlane(wave & 1) == 0) {
-        dpair_half<D, 0, C::DA>(p, smem, wave);
+        dpair_half<D, PRE, 0, C::DA>(p, smem, wave);
     } else {
-        dpair_half<D, C::DA, C::DB>(p, smem, wave);
+        dpair_half<D, PRE, C::DA, C::DB>(p, smem, wave);
     }
 }
 
 template <int D>
 int launch_dpair_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL((fa_fwd_f16_dpair<D>), dim3((uint32_t)n_wg), dim3(kDPThreads), 0, stream, p);
+    // Q pre-scaled into log2 units when |q| c stays representable (c <= 1); not
+    // above D = 448, where the 16 registers of half 0's accumulator start do
+    // not fit
+    constexpr bool kPre = D <= 448;
+    if (kPre && p.c <= 1.0f) {
+        hipLaunchKernelGGL((fa_fwd_f16_dpair<D, kPre>), dim3((uint32_t)n_wg), dim3(kDPThreads), 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((fa_fwd_f16_dpair<D, false>), dim3((uint32_t)n_wg), dim3(kDPThreads), 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -480,6 +504,9 @@ int launch_dpair_d(const PrefillParams& p, int64_t n_wg, hipStream_t stream, std
 
 int launch_dpair(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err) {
     switch (head_dim) {
+    case 288: return launch_dpair_d<288>(p, n_wg, stream, err);
+    case 320: return launch_dpair_d<320>(p, n_wg, stream, err);
+    case 352: return launch_dpair_d<352>(p, n_wg, stream, err);
     case 384: return launch_dpair_d<384>(p, n_wg, stream, err);
     case 416: return launch_dpair_d<416>(p, n_wg, stream, err);
     case 448: return launch_dpair_d<448>(p, n_wg, stream, err);

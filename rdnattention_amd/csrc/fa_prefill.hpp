@@ -40,18 +40,13 @@ struct PrefillParams {
 // (kv_bytes each) fit its L2; 0 when the grid cannot be dealt evenly.
 int xcd_head_group_chunk(int n_head_groups, int64_t kv_bytes);
 
-// Large-head prefill for head_dim 288..kWideMaxD (fa_fwd_f16_wide.hip):
-// workgroups of 4 waves, each wave 32 rows of one head.
-constexpr int kWideMaxD = 352;
-int launch_wide(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
-
 // Prefill for head_dim 160..256 (fa_fwd_f16_kpair.hip): 8 waves, each pair of
 // waves 32 rows of one head, so a workgroup holds kKPairRows / G rows of G
 // heads (the launcher's PrefillParams must be set up that way).
 constexpr int kKPairRows = 128;
 int launch_kpair(const PrefillParams& p, int head_dim, int64_t n_wg, hipStream_t stream, std::string& err);
 
-// Prefill for head_dim 384..512 (fa_fwd_f16_dpair.hip): 8 waves, each pair of
+// Prefill for head_dim 288..512 (fa_fwd_f16_dpair.hip): 8 waves, each pair of
 // waves 32 rows of one head with the head dimension split between them, so a
 // workgroup holds kDPairRows / G rows of G heads (the launcher's
 // PrefillParams must be set up that way).

@@ -25,7 +25,6 @@ WAVES_PER_SIMD = {
     "fa_fwd_f16_pp": 2,
     "fa_fwd_int8": 2,
     "fa_fwd_f16_kpair": 2,
-    "fa_fwd_f16_wide": 1,
     "fa_fwd_f16_dpair": 2,
     "fa_fwd_f16_decode": 1,
 }
@@ -62,7 +61,7 @@ def test_occupancy_fits_the_workgroup(kernels):
         if need is not None:
             assert k["waves_per_simd"] >= need, (k["kernel"], k["waves_per_simd"], need)
             checked += 1
-    # pp 4, kpair 4, wide 3 + dpair 5, decode 3, int8 4 (+ 2 score-export instantiations)
+    # pp 4, kpair 4, dpair 8, decode 3, int8 4 (+ 2 score-export instantiations)
     assert checked >= 4 + 4 + 3 + 5 + 3 + 4
 
 
@@ -76,9 +75,7 @@ def test_every_dispatched_head_dim_is_compiled(kernels):
         assert has("fa_fwd_f16_pp", d), d
     for d in (160, 192, 224, 256):
         assert has("fa_fwd_f16_kpair", d), d
-    for d in (288, 320, 352):
-        assert has("fa_fwd_f16_wide", d), d
-    for d in range(384, 513, 32):
+    for d in range(288, 513, 32):
         assert has("fa_fwd_f16_dpair", d), d
     for d in (32, 64, 128):
         assert has("fa_fwd_f16_decode", d), d
