@@ -28,9 +28,11 @@
 // the loop.  K/V tiles of 32 keys move HBM -> LDS by buffer_load ... lds, one
 // DMA instruction per row into padded rows (K at D + 8 halves, V at = 32 mod
 // 128 halves: the 16-row ds_read_b128 of K and the 4-row transpose reads of V
-// hit distinct banks), double-buffered.  The DMAs of pair x + 2 (K(x+2),
-// V(x+1)) are issued by group B's half-1 waves, whose softmax phase is
-// otherwise empty, two phases before the pair is read.  Key tiles are walked
+// hit distinct banks), double-buffered.  The half-1 waves, whose softmax
+// phase is otherwise empty, issue the DMAs there: group B's the K tiles two
+// phases before they are read, group A's the V tiles one phase before; with
+// the issue split over four waves a tile's DMAs are in flight sooner than
+// from two (D 384 +4-5 %, c5b +0.7 %).  Key tiles are walked
 // from the aligned start of fa_fwd_f16_kpair.hip, skipped outside the
 // causal/window band and masked only at its edges.
 #include "fa_common.hpp"
@@ -99,8 +101,12 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
     f4* const xs = reinterpret_cast<f4*>(xpair);
     h8* const xp = reinterpret_cast<h8*>(xpair);
     float* const xa = reinterpret_cast<float*>(xpair + C::XS_BYTES);
-    // group B's half-1 waves issue every K/V DMA
-    const bool dma_wave = HALF == 1 && grp == 1;
+    // group B's half-1 waves issue the K DMAs, group A's the V DMAs; the group
+    // is read from the first lane so that these branches, and the DMA
+    // addresses inside them, are scalar
+    const int grp_u = __builtin_amdgcn_readfirstlane(grp);
+    const bool dma_k = HALF == 1 && grp_u == 1;
+    const bool dma_v = HALF == 1 && grp_u == 0;
 
     const int wg = blockIdx.x;
     int hg, rt;
@@ -153,8 +159,8 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
     // both halves of a pair share rows, so they share tile classes
     const TileClasses tcls = wave_active ? tile_classes<kDPBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
-    // DMAs of pair x: rows dma_r0 .. dma_r0 + 15 of K(x) (x < n) and of
-    // V(x - 1) (1 <= x <= n), lane i moving bytes 16i .. 16i+15 of each row.
+    // DMAs of a K or V tile: rows dma_r0 .. dma_r0 + 15, lane i moving bytes
+    // 16i .. 16i+15 of each row.
     // The row offsets and LDS row addresses are wave-uniform and stepped row by
     // row in scalar registers from an opaque start, so that no per-row value is
     // precomputed and kept across the key-tile loop.
@@ -175,25 +181,26 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
             }
         }
     };
-    auto issue_pair = [&](int x) {
-        auto uniform = [](i32x4_t r) {
-            for (int e = 0; e < 4; e++) {
-                r[e] = __builtin_amdgcn_readfirstlane(r[e]);
-            }
-            return r;
-        };
-        if (x < n) {
-            const int kt0 = walk(x) * kDPBN;
-            const i32x4_t rk = uniform(
-                make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kDPBN>(p.mask.sk - kt0, k_row_b, D * 2)));
-            issue_rows(rk, k_row_b, lds0 + (uint32_t)((x & 1) * C::TILE_K * 2), C::LDK * 2);
+    auto uniform = [](i32x4_t r) {
+        for (int e = 0; e < 4; e++) {
+            r[e] = __builtin_amdgcn_readfirstlane(r[e]);
         }
-        if (x >= 1 && x <= n) {
-            const int vt0 = walk(x - 1) * kDPBN;
-            const i32x4_t rv = uniform(
-                make_rsrc_v(vbase + (int64_t)vt0 * p.v_ss, tile_bytes<kDPBN>(p.mask.sk - vt0, v_row_b, D * 2)));
-            issue_rows(rv, v_row_b, lds0 + (uint32_t)((2 * C::TILE_K + ((x - 1) & 1) * C::TILE_V) * 2), C::LDV * 2);
-        }
+        return r;
+    };
+    // K(x) into K slot x % 2 (x < n); V(x) into V slot x % 2 (x < n)
+    auto issue_k = [&](int x0) {
+        const int x = __builtin_amdgcn_readfirstlane(x0);
+        const int kt0 = walk(x) * kDPBN;
+        const i32x4_t rk = uniform(
+            make_rsrc_v(kbase + (int64_t)kt0 * p.k_ss, tile_bytes<kDPBN>(p.mask.sk - kt0, k_row_b, D * 2)));
+        issue_rows(rk, k_row_b, lds0 + (uint32_t)((x & 1) * C::TILE_K * 2), C::LDK * 2);
+    };
+    auto issue_v = [&](int x0) {
+        const int x = __builtin_amdgcn_readfirstlane(x0);
+        const int vt0 = walk(x) * kDPBN;
+        const i32x4_t rv = uniform(
+            make_rsrc_v(vbase + (int64_t)vt0 * p.v_ss, tile_bytes<kDPBN>(p.mask.sk - vt0, v_row_b, D * 2)));
+        issue_rows(rv, v_row_b, lds0 + (uint32_t)((2 * C::TILE_K + (x & 1) * C::TILE_V) * 2), C::LDV * 2);
     };
 
     // Q^T operand of d-range [C0, C0 + W): lane holds Q[q][C0 + 16s + 8g .. +7]
@@ -389,43 +396,48 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
         }
     };
 
-    // Prologue: pairs 0 and 1 in flight, pair 0 landed before the first barrier
-    if (dma_wave && n > 0) {
-        issue_pair(0);
-        issue_pair(1);
-        if (n >= 2) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * C::DMA_ROWS)); // pair 1's K and V rows may be outstanding
-        } else {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-        }
+    // Prologue: K(0) landed before the first barrier
+    if (dma_k && n > 0) {
+        issue_k(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
     __syncthreads();
     // Group A: M(i) in phase 2i, V(i) in phase 2i + 1; group B one phase later.
-    // Pair x + 2 reuses the slots of pair x, which both groups have read by
-    // the end of phase 2x + 1: its DMAs are issued at the start of phase
-    // 2x + 2 (group B's V(x)) and waited for at the end of phase 2x + 3
-    // (group B's M(x + 1)).  Both groups pass 2n + 2 barriers.
+    // K(i) is read in phases 2i and 2i + 1, V(i) in 2i + 2 and 2i + 3.  K(i + 2)
+    // reuses K(i)'s slot: group B's half-1 waves issue it at the start of phase
+    // 2i + 2 and wait for it at the end of phase 2i + 3.  V(i) reuses V(i - 2)'s
+    // slot: group A's half-1 waves issue it at the start of phase 2i + 1 and
+    // wait for it at the end of that phase.  Both groups pass 2n + 2 barriers.
     if (n > 0) {
         if (grp == 0) {
             for (int i = 0; i < n; i++) {
                 phase_m(i);
                 __syncthreads();
+                if (dma_v) {
+                    issue_v(i);
+                }
                 phase_v(i);
+                if (dma_v) {
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // V(i) landed
+                }
                 __syncthreads();
             }
             phase_m(n);
             __syncthreads();
             __syncthreads();
         } else {
+            if (dma_k && 1 < n) {
+                issue_k(1);
+            }
             __syncthreads();
             for (int i = 0; i < n; i++) {
                 phase_m(i);
-                if (dma_wave) {
-                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // pair i + 1 landed
+                if (dma_k) {
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed
                 }
                 __syncthreads();
-                if (dma_wave && i + 2 <= n) {
-                    issue_pair(i + 2);
+                if (dma_k && i + 2 < n) {
+                    issue_k(i + 2);
                 }
                 phase_v(i);
                 __syncthreads();
