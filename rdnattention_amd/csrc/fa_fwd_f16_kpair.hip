@@ -255,9 +255,11 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         float ps_own = 0.0f;      // own row sum of the P held in pb
         int cls_prev = 0;         // class of the tile whose P is held in pb
 
-        // M(i): O^T += V(i-1)^T P(i-1)^T (i >= 1), then S(i)^T = K(i) Q^T for the
-        // own 32 keys (i < n), as one stream of MFMAs whose LDS operands are read
-        // C::OP_DEPTH MFMAs ahead through a register ring
+        // M(i): S(i)^T = K(i) Q^T for the own 32 keys (i < n), then O^T +=
+        // V(i-1)^T P(i-1)^T (i >= 1), as one stream of MFMAs whose LDS operands
+        // are read C::OP_DEPTH MFMAs ahead through a register ring.  Q K^T first:
+        // the partner's P^T, read from LDS as the phase starts, is not needed
+        // before the P V MFMAs, and the own scores are done by the phase's end.
         auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
             constexpr bool DO_PV = decltype(do_pv_c)::value;
             constexpr bool DO_S = decltype(do_s_c)::value;
@@ -276,14 +278,14 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 pop[1] = xp[(partner * 2 + 1) * 64 + lane];
             }
             auto op = [&](int j) -> h8 {
-                if (j < NPV) {
-                    const int u = j / NDT, dt = j % NDT;
-                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                    h4 lo = lds_read_tr16(base);
-                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                if (j < NSK) {
+                    return *reinterpret_cast<const h8*>(krow + 16 * j);
                 }
-                return *reinterpret_cast<const h8*>(krow + 16 * (j - NPV));
+                const int jv = j - NSK, u = jv / NDT, dt = jv % NDT;
+                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
             };
             f16x acc = {};
             h8 ring[DEPTH > 0 ? DEPTH : 1];
@@ -297,13 +299,12 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 if (j + DEPTH < T) {
                     ring[j % DEPTH] = op(j + DEPTH);
                 }
-                if (j < NPV) {
-                    const int u = j / NDT, dt = j % NDT;
+                if (j < NSK) {
+                    acc = mfma_32x32x16_f16(a, qreg[j], (PRE && j == 0) ? minit : acc);
+                } else {
+                    const int jv = j - NSK, u = jv / NDT, dt = jv % NDT;
                     const h8 pu = (u >> 1) == HALF ? pb[u & 1] : pop[u & 1];
                     oacc[dt] = mfma_32x32x16_f16(a, pu, oacc[dt]);
-                } else {
-                    const int st = j - NPV;
-                    acc = mfma_32x32x16_f16(a, qreg[st], (PRE && st == 0) ? minit : acc);
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -317,12 +318,9 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             }
             const bool do_pv = i >= 1 && cls_prev != 0;
             const int cls_now = i < n ? tile_class(tcls, walk(i)) : 0;
-            if (do_pv) {
-                // the pair's row sum of tile i-1: the same two terms in the same
-                // order in both halves
-                const float po = xsum[partner * 64 + lane];
-                l_run += HALF == 0 ? ps_own + po : po + ps_own;
-            }
+            // the partner's row sum of tile i-1, read now and added after the
+            // MFMAs so that the LDS round trip does not hold up the stream
+            const float po = do_pv ? xsum[partner * 64 + lane] : 0.0f;
             using T_ = std::true_type;
             using F_ = std::false_type;
             if (do_pv && cls_now != 0) {
@@ -331,6 +329,11 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 mfma_stream(T_{}, F_{}, i);
             } else if (cls_now != 0) {
                 mfma_stream(F_{}, T_{}, i);
+            }
+            if (do_pv) {
+                // the pair's row sum of tile i-1: the same two terms in the same
+                // order in both halves
+                l_run += HALF == 0 ? ps_own + po : po + ps_own;
             }
             if (cls_now != 0) {
                 if (cls_now == 2) {
