@@ -96,11 +96,17 @@ WORKLOADS = {
     "fp16_mha_b1_h8_s512_d64":
         Workload("f16", 1, 8, 8, 512, 512, 64, False, -1, False, 0, 1.0, "fa_fwd_f16_pp<64, true>"),
     "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128":
-        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, false, false>"),
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8_f16pv<128, false, false>"),
     "int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128":
-        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8<128, true, false>", True),
+        Workload("int8", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_int8_f16pv<128, true, false>",
+                 True),
     "fp16_causal_gqa_b2_h32_kv8_s8192_d128":
         Workload("f16", 2, 32, 8, 8192, 8192, 128, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<128, true>"),
+    # the same shape at head_dim 64, where the INT8 kernel runs both GEMMs on int8 MFMA
+    "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d64":
+        Workload("int8", 2, 32, 8, 8192, 8192, 64, True, -1, False, 3, 1.0, "fa_fwd_int8<64, true, false>"),
+    "fp16_causal_gqa_b2_h32_kv8_s8192_d64":
+        Workload("f16", 2, 32, 8, 8192, 8192, 64, True, -1, False, 3, 1.0, "fa_fwd_f16_pp<64, true>"),
     "fp16_decode_b16_h32_kv8_sq1_sk32768_d128":
         Workload("decode", 16, 32, 8, 1, 32768, 128, False, -1, False, 4, 1.0, "fa_fwd_f16_decode<128>"),
     "fp16_decode_b16_h32_kv8_sq4_sk32768_d128":
@@ -115,6 +121,8 @@ SECONDARY = [
     "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d128",
     "int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128",
     "fp16_causal_gqa_b2_h32_kv8_s8192_d128",
+    "int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d64",
+    "fp16_causal_gqa_b2_h32_kv8_s8192_d64",
     "fp16_decode_b16_h32_kv8_sq1_sk32768_d128",
     "fp16_decode_b16_h32_kv8_sq4_sk32768_d128",
     "fp16_window4096_rope_b1_h16_s16384_d256",
@@ -672,6 +680,10 @@ def main(argv=None):
         f16 = secondary.get("fp16_causal_gqa_b2_h32_kv8_s8192_d128", {})
         if "kernel_ms" in i8 and "kernel_ms" in f16:
             secondary["int8_over_fp16_same_shape"] = round(f16["kernel_ms"] / i8["kernel_ms"], 3)
+        i8d64 = secondary.get("int8_causal_gqa_pertoken_b2_h32_kv8_s8192_d64", {})
+        f16d64 = secondary.get("fp16_causal_gqa_b2_h32_kv8_s8192_d64", {})
+        if "kernel_ms" in i8d64 and "kernel_ms" in f16d64:
+            secondary["int8_over_fp16_same_shape_d64"] = round(f16d64["kernel_ms"] / i8d64["kernel_ms"], 3)
         i8t = secondary.get("int8_causal_gqa_pertoken_vtoken_b2_h32_kv8_s8192_d128", {})
         if "kernel_ms" in i8 and "kernel_ms" in i8t:
             secondary["int8_vtoken_time_over_int8"] = round(i8t["kernel_ms"] / i8["kernel_ms"], 3)

@@ -229,6 +229,16 @@ __device__ __forceinline__ void dma_load16(i32x4_t rsrc, uint32_t voff, uint32_t
                  : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
                  : "memory", "m0");
 }
+// HBM -> LDS copy of 4 bytes per lane (buffer_load_dword ... lds): lane i
+// reads the dword at voff and writes LDS bytes [lds + 4 i, lds + 4 i + 4).
+// Each lane's dword is range-checked on its own, so a vector of floats that
+// ends inside a 16-byte chunk is copied exactly.
+__device__ __forceinline__ void dma_load4(i32x4_t rsrc, uint32_t voff, uint32_t lds_byte_addr) {
+    asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(lds_byte_addr)
+                 : "memory", "m0");
+}
 // dma_load16 with a wave-uniform byte offset `soff` (the instruction's scalar
 // offset) added to voff: a loop over rows then keeps one vector offset.
 __device__ __forceinline__ void dma_load16_s(i32x4_t rsrc, uint32_t voff, uint32_t soff, uint32_t lds_byte_addr) {

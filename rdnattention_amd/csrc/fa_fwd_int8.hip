@@ -1,43 +1,47 @@
-// INT8 FlashAttention forward for gfx950: Q K^T on int8 MFMA
-// (v_mfma_i32_32x32x32_i8, exact int32 accumulation), P V on fp16 MFMA,
-// fp16 output.
+// INT8 FlashAttention forward for gfx950 at head_dim 64: Q K^T and P V both on
+// int8 MFMA (v_mfma_i32_32x32x32_i8, exact int32 accumulation), fp16 output.
+// Head_dim 128 and the per-token V scale run fa_fwd_int8_f16pv.hip (P V on
+// fp16 MFMA; its header gives the measured reason).  This file also holds the
+// INT8 host entry (fwd_int8, the score export, the launch parameters).
 //
 // Replaces the reference's forwardKernelInt8QK
 // (src/rdna/fa2_forward_int8qk.hip:229-495) and keeps its numeric scheme:
 //
-//   S_ij  = sum_d q_i8 k_i8                          (exact int32)
-//   s_ij  = S_ij * qs_i * ks_j * scale * log2(e)      (fp32, log2 domain)
+//   S_ij  = sum_d q_i8 k_i8                          (exact int32, :254-278)
+//   s_ij  = S_ij * qs_i * ks_j * scale * log2(e)      (fp32, log2 domain, :301)
 //   per 64-key block, aligned to key 0 (the reference's Bc = 64):
 //     m'  = max(m, max_j s_ij);  O *= 2^(m - m'),  l *= 2^(m - m')
 //     p   = 2^(s - m'),  l += sum p                  (unquantised p)
 //     pq  = min(127, round(p * 127))                 (P as integers 0..127)
-//     O  += sum_j pq_j v_j
+//     O  += sum_j pq_j v_j                           (exact int32, :354-382)
 //   out = O * v_scale / (127 l)  (0 when no key is visible)
 //
-// The running max m is exact per block, as the scheme requires (pq depends
-// on it).  O and l are instead kept relative to a lagging reference m_ref <=
-// m, raised only when m exceeds it by more than 2^8: each block's P enters
-// the P V product as pq * fp16(2^(m - m_ref)) (packed fp16 multiplies, one
-// rounding, values <= 127 * 256) and its row sum as sum p * that same factor,
-// so O / l is the scheme's ratio while the 64-accumulator rescale of O runs
-// only when the reference moves.  P V runs on fp16 MFMA: the products of
-// these fp16 P values and the int8 V values (exact in fp16) are exact in
-// fp32.
+// O is held as O_f * 2^(m_a - m_c) + O_int: O_int is the int32 accumulator of
+// the P V MFMAs, the exact sum of every block since the running maxima of the
+// wave's 32 query rows last moved (all relative to the current maxima m_c),
+// and O_f (fp32, relative to m_a) holds everything before.  While no row
+// maximum moves, blocks accumulate in int32 with no VALU work at all; when one
+// moves, the wave folds O_int into O_f once (one conversion and one fma per
+// accumulator) and restarts the int32 chain.  Each block's sum is therefore
+// the reference's exact int32 sum, and its weight 2^(m_b - m_final) is applied
+// in fp32 as the reference's per-block rescale does.
 //
 // Deliberate differences, all far below the INT8 tolerance: round() is
-// round-half-to-even (v_rndne_f32) where the reference calls lroundf (half
-// away from zero), 127 p is evaluated as 2^(s - m' + log2 127), the per-block
-// v_scale/127 factor is applied once at the end, and P is scaled by the
-// reference factor above (relative rounding <= 2^-12 per element).
+// round-half-to-even (v_cvt_pk_u8_f32) where the reference calls lroundf
+// (half away from zero), 127 p is evaluated as 2^(s - m' + log2 127) (at most
+// 127 plus rounding, so the min(127) never binds), s is formed as
+// (S * ks) * (qs * scale * log2(e)), and v_scale/127 is applied once at the end.
 //
-// Kernel structure is the FP16 ping-pong design (fa_fwd_f16.hip): 8 waves in
-// two groups alternating MFMA and VALU phases, S^T = K Q^T so a lane owns one
-// query column, and P^T going from the S accumulator straight into the B
-// operand of O^T = V^T P^T.  V is converted to fp16 while it is staged into
-// LDS (a byte permute against the fp16 exponent of 1024, then one packed
-// subtract) and its V^T operands come from ds_read_b64_tr_b16 transpose
-// reads.  The grid is persistent (persistent_item), and O leaves through an
-// LDS buffer as whole-row non-temporal stores (store_o_tile).
+// Kernel structure: 8 waves in two groups of four that alternate an MFMA phase
+// (P V of the previous tile, Q K^T of this one) and a softmax phase, S^T = K Q^T
+// so that a lane owns one query column, and P^T going from the softmax straight
+// into the B operand of O^T = V^T P^T as packed bytes.  K, V and the per-token
+// K scales go from HBM to LDS by DMA (buffer_load ... lds), issued by group A
+// two tiles ahead into four tile slots, so neither group stages anything
+// through registers.  Tiles are stored unpadded with 16-byte chunks swizzled
+// per row (i8_swz); the V^T operands come from ds_read_b64_tr_b8 transpose
+// reads.  The grid is persistent (persistent_item), and O leaves through an LDS
+// buffer as whole-row non-temporal stores (store_o_tile).
 //
 // SCORES (a test instantiation): the same kernel with the softmax, P V and
 // output compiled out; every S^T accumulator block its first GEMM produces is
@@ -45,6 +49,7 @@
 // GEMM's scores bit for bit.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
+#include "fa_int8.hpp"
 #include "fa_internal.hpp"
 #include "fa_prefill.hpp"
 
@@ -56,127 +61,72 @@ namespace rdna_amd {
 
 #if !defined(RDNATTENTION_NO_INT8)
 
-float softmax_log2_scale(float scale);
-
 namespace {
 
-typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
 typedef int i2 __attribute__((ext_vector_type(2)));
 
-constexpr int kI8Waves = 8;
-constexpr int kI8Threads = 64 * kI8Waves;
-constexpr int kI8BN = 64; // keys per tile = the reference's max-update block
-
-struct Int8Params {
-    const int8_t* q;
-    const int8_t* k;
-    const int8_t* v;
-    _Float16* o;
-    const float* qsv; // [B, Hq, Sq] or null
-    const float* ksv; // [B, Hkv, Sk] or null
-    const float* vch; // [B, Hkv, D] per-channel V scale or null
-    const float* vtok; // [B, Hkv, Sk] per-token V scale (the VTOK kernel) or null
-    int32_t* scores;   // [B, Hq, Sq, Sk] int32 (the SCORES instantiation only)
-    float q_scale, k_scale;
-    float v_scale;
-    float scale_log2e;
-    int64_t q_sb, q_sh, q_ss;
-    int64_t k_sb, k_sh, k_ss;
-    int64_t v_sb, v_sh, v_ss;
-    int64_t o_sb, o_sh, o_ss;
-    int32_t Hq, Sq, Hkv, ratio, G, rows_per_wg, n_row_tiles, n_head_groups, groups_per_kv;
-    int32_t hg_chunk; // head groups per XCD at a time (0 = head groups fastest)
-    int32_t n_items;  // n_row_tiles * n_head_groups
-    MaskSpec mask;
-};
+constexpr int kI8Slots = 4;                  // K/V tile slots in LDS (DMAs run two tiles ahead)
+constexpr int kI8OpDepth = 4;                // LDS operands in flight in the MFMA phase
+constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
 
 template <int D>
 struct I8Cfg {
-    // K: int8 rows of D bytes at a D+16 byte stride (16 rows read with
-    // ds_read_b128 land in distinct banks); V: converted to fp16 while staged,
-    // rows at D+32 halves (conflict-free 4-row transpose reads)
-    static constexpr int LDK = D + 16;         // bytes
-    static constexpr int LDV = D + 32;         // halves
-    static constexpr int TILE_K = kI8BN * LDK; // bytes
-    static constexpr int TILE_V = kI8BN * LDV; // halves
-    static constexpr int NS = D / 32;          // int8 QK^T reduction steps (32 per MFMA)
-    static constexpr int NDT = D / 32;         // O^T row tiles
-    static constexpr int KCH = D / 16;         // 16-byte int8 chunks per row
-    static constexpr int HALF_TASK = 32 * KCH; // one group's chunks of one K (or V) tile
-    static constexpr int CT = (HALF_TASK + 255) / 256;
-    static constexpr int LDO = D + 8; // halves; output staging rows (conflict-free like K rows)
+    // One wave per 32 query rows holds 32 + 32 O^T accumulators (int32 and
+    // fp32) at D = 64; at D = 128 they would take 128 registers (see the
+    // header), so this kernel is built for D = 64 only.
+    static_assert(D == 64, "head_dim 128 runs fa_fwd_int8_f16pv");
+    static constexpr int CH = D / 16;          // 16-byte chunks per int8 row
+    static constexpr int TILE = kI8BN * D;     // bytes of one K (or V) tile, rows unpadded
+    static constexpr int BLOCKS = TILE / 1024; // 1 KB DMA blocks (64 lanes x 16 bytes) per tile
+    static constexpr int BPW = BLOCKS / 4;     // blocks per issuing wave (group A's four waves)
+    static constexpr int NS = D / 32;          // Q K^T reduction steps (32 per MFMA)
+    static constexpr int NDT = D / 32;         // O^T row tiles (32 columns each)
+    static constexpr int QB = 32 * D / 1024;   // DMA blocks of one wave's 32 Q rows
+    static constexpr int LDO = D + 8;          // halves; output staging rows (conflict-free)
+    static_assert(BLOCKS % 4 == 0 && BPW >= 1 && QB >= 1, "tiles split into whole DMA blocks per wave");
+    static_assert(NS * 2 * 8 == 16 * NDT, "the fold rides on the Q K^T MFMAs, 8 accumulators each");
 };
 
-constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
-constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
-constexpr float kI8RefThreshold = 8.0f;      // log2 units: P is scaled by at most 2^8 (127 * 256 < 65504)
-
-__device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-    typedef unsigned u4 __attribute__((ext_vector_type(4)));
-    u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
-    return __builtin_bit_cast(i4, x);
+// Chunk swizzle of the K, V and Q tiles in LDS (64-byte rows): byte b of
+// 16-byte chunk c of tile row r sits at r * 64 + 16 * (c ^ i8_swz(r)) + b.
+// The two read patterns then use every bank once per 256 bytes:
+//   K and Q operands (ds_read_b128): 16 consecutive rows, one chunk;
+//   V^T operand (ds_read_b64_tr_b8): rows {0-3, 8-11} + 4 g, two adjacent
+//   chunks, two 8-byte halves each, over 32 lanes.
+// The swizzle depends only on row bits 2-3, so rows 16 and 32 apart share it.
+__host__ __device__ constexpr int i8_swz(int r) {
+    return (r >> 2) & 3;
 }
 
-// 16 signed bytes -> two h8 (exact: every int8 is an fp16 integer).  Flipping
-// the sign bit gives u = v + 128 as an unsigned byte; a byte permute pairs each
-// u with the high byte 0x64, i.e. the fp16 value 1024 + u (exact: the ulp in
-// [1024, 2048) is 1), and one packed subtract of 1152 leaves v.  Five VALU
-// instructions per 4 values.
-__device__ __forceinline__ void i8x16_to_h8x2(i4 w, h8& lo, h8& hi) {
-    const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    h2 r[8];
+// ds_read_b64_tr_b8 (gfx950 LDS transpose read).  Within each 16-lane group,
+// lane i receives as byte k the byte (i % 8) of the 8-byte word whose address
+// lane 2k + i / 8 supplies: if lane j points at row j / 2, bytes 8 (j % 2) ..
+// +7 of an 8-row x 16-byte block, lane i gets column i of the block, the
+// eight rows' bytes in order.
+__device__ __forceinline__ i2 lds_read_tr8(const int8_t* p) {
+    typedef __attribute__((address_space(3))) i2 lds_i2;
+    const auto* lp = reinterpret_cast<const __attribute__((address_space(3))) char*>(
+        (uint32_t)reinterpret_cast<uintptr_t>(p));
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i2*)lp);
+}
+
+__device__ __forceinline__ i32x4_t uniform_rsrc(i32x4_t r) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const uint32_t u = (uint32_t)w[c] ^ 0x80808080u;
-        // byte selects: 0-3 pick bytes of u, 4 picks byte 0 of 0x64646464
-        const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
-        const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
-        r[2 * c] = __builtin_bit_cast(h2, p01) - off;
-        r[2 * c + 1] = __builtin_bit_cast(h2, p23) - off;
+    for (int e = 0; e < 4; e++) {
+        r[e] = __builtin_amdgcn_readfirstlane(r[e]);
     }
-    lo = {r[0][0], r[0][1], r[1][0], r[1][1], r[2][0], r[2][1], r[3][0], r[3][1]};
-    hi = {r[4][0], r[4][1], r[5][0], r[5][1], r[6][0], r[6][1], r[7][0], r[7][1]};
+    return r;
 }
 
-// 16 signed bytes of one V row -> two h8 of fp16(sat(v * vs)): the product in
-// fp32 (v exact, vs as given), saturated to the fp16 range so that no V value
-// becomes infinite (a zero P times an infinite V would be NaN for every row
-// sharing the tile), then rounded once to fp16
-__device__ __forceinline__ void i8x16_to_h8x2_scaled(i4 w, float vs, h8& lo, h8& hi) {
-    const i8x8 a = __builtin_bit_cast(i8x8, i2{w[0], w[1]});
-    const i8x8 b = __builtin_bit_cast(i8x8, i2{w[2], w[3]});
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        lo[e] = (_Float16)__builtin_amdgcn_fmed3f((float)a[e] * vs, -65504.0f, 65504.0f);
-        hi[e] = (_Float16)__builtin_amdgcn_fmed3f((float)b[e] * vs, -65504.0f, 65504.0f);
-    }
-}
-
-// Scheme (the reference's, fa2_forward_int8qk.hip:281-382), per 64-key block b
-// aligned to key 0, with s_j = S_j * qs * ks_j * scale * log2(e):
-//   m_b  = max(m_{b-1}, max_j s_j)     (exact: pq below depends on it)
-//   y_j  = 127 * 2^(s_j - m_b)         (computed as 2^(s_j - m_b + log2 127))
-//   pq_j = round(y_j) in [0, 127]
-//   f_b  = fp16(2^(m_b - m_ref))       (m_ref <= m_b: raised, with O and l
-//                                       rescaled, only when m_b - m_ref > 8)
-//   l   += f_b * sum_j y_j              (unquantised p, in units of 1/127)
-//   O   += sum_j fp16(pq_j * f_b) v_j
-//   out  = O * v_scale / l
-// S runs on int8 MFMA (exact int32).  P V runs on fp16 MFMA and accumulates
-// straight into fp32, so O needs no per-block int32 -> fp32 conversion.
-//
-// VTOK (an extension; the reference has no per-token V scale): V row j is
-// dequantised by its own scale vs_j while it is staged,
-// v'_j = fp16(sat(v_j * vs_j)), and P V runs on these fp16 values.
-//
-// SCORES: the S^T accumulators of every computed key tile are written to
-// p.scores and nothing else is computed (test instantiation).
-template <int D, bool VTOK, bool SCORES>
+// KSV: per-token K scales (p.ksv) staged per tile; otherwise p.k_scale is
+// folded into the per-row factor.
+template <int D, bool KSV, bool SCORES>
 __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     using C = I8Cfg<D>;
-    __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
-    __shared__ __attribute__((aligned(16))) _Float16 sVs[2 * C::TILE_V];
-    __shared__ __attribute__((aligned(16))) float sks[2][kI8BN];
+    // [slot][K, V][TILE]; DMA destinations, so the base is 1 KB aligned
+    __shared__ __attribute__((aligned(1024))) int8_t sKV[kI8Slots * 2 * C::TILE];
+    __shared__ __attribute__((aligned(1024))) int8_t sQ[kI8Waves * 32 * D]; // [wave][32 rows][D], swizzled
+    __shared__ __attribute__((aligned(16))) float sks[kI8Slots * kI8BN];
     __shared__ __attribute__((aligned(16))) _Float16 sO[kI8Waves * 32 * C::LDO];
 
     const int tid = threadIdx.x;
@@ -185,13 +135,44 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     const int l32 = lane & 31;
     const int g = lane >> 5;
     const int grp = wave >> 2;
-    const int gtid = tid & 255;
+    const uint32_t kv_lds = (uint32_t)reinterpret_cast<uintptr_t>(sKV);
+    const uint32_t ks_lds = (uint32_t)reinterpret_cast<uintptr_t>(sks);
 
-    // Persistent: this workgroup walks its share of the row tiles (one per
-    // workgroup of a one-tile-per-workgroup grid, see persistent_item). Every
-    // group passes the same barriers per tile and leaves a tile only after its
-    // last LDS read of K/V, so the next tile's prologue may overwrite them;
-    // each wave's sO slot is its own.
+    // LDS operand offsets within a tile, fixed per lane:
+    //   K (and Q) operand of reduction step st (+ 32 D for keys 32..63): row
+    //   l32, chunk 2 st + g;
+    //   V^T operand of O^T row tile dt: lane j of a 16-lane group reads the 8 bytes
+    //   8 (j & 1) .. +7 of chunk 2 dt + (lane >> 4 & 1) in key row kb(j) (+ 16 D for
+    //   the second read, + 32 D for keys 32..63), kb = 8 (j/2 / 4) + 4 g + (j/2 % 4).
+    int kofs[C::NS], vofs[C::NDT];
+    {
+        const int sw = i8_swz(l32);
+#pragma unroll
+        for (int st = 0; st < C::NS; st++) {
+            kofs[st] = l32 * D + 16 * ((2 * st + g) ^ sw);
+        }
+        const int k8 = (lane & 15) >> 1;
+        const int kb = 8 * (k8 >> 2) + 4 * g + (k8 & 3);
+        const int swv = i8_swz(kb);
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; dt++) {
+            vofs[dt] = kb * D + 16 * ((2 * dt + ((lane >> 4) & 1)) ^ swv) + 8 * (lane & 1);
+        }
+    }
+    // DMA source offsets of this lane in the BPW blocks a group-A wave issues per
+    // tile: physical chunk P = 64 (wave BPW + jj) + lane holds row P / CH, logical
+    // chunk (P % CH) ^ swz(row)
+    uint32_t dk[C::BPW], dv[C::BPW];
+#pragma unroll
+    for (int jj = 0; jj < C::BPW; jj++) {
+        const int P = 64 * ((wave & 3) * C::BPW + jj) + lane;
+        const int r = P / C::CH;
+        const int c = (P % C::CH) ^ i8_swz(r);
+        dk[jj] = (uint32_t)((int64_t)r * p.k_ss + 16 * c);
+        dv[jj] = (uint32_t)((int64_t)r * p.v_ss + 16 * c);
+    }
+    constexpr int DPT = 2 * C::BPW; // K/V DMAs per group-A wave per tile (wave 0 adds one for the K scales)
+
     auto run_tile = [&](const int wg) {
         int hg, rt;
         wg_tile(wg, p.n_head_groups, p.n_row_tiles, p.hg_chunk, hg, rt);
@@ -212,27 +193,17 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         const int8_t* kbase = p.k + b * p.k_sb + kvh * p.k_sh;
         const int8_t* vbase = p.v + b * p.v_sb + kvh * p.v_sh;
         _Float16* obase = p.o + b * p.o_sb + h * p.o_sh;
-        const float* ksbase = p.ksv ? p.ksv + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
-        const float* vtbase = VTOK ? p.vtok + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
+        const float* ksbase = KSV ? p.ksv + ((int64_t)b * p.Hkv + kvh) * Sk : nullptr;
 
-        // Q^T operand: lane holds Q[q][32s + 16g .. +15]
-        i4 qreg[C::NS];
         float qs = p.q_scale;
-        {
-            const bool valid = q < p.Sq;
-            const int8_t* qrow = qbase + (int64_t)(valid ? q : 0) * p.q_ss;
-#pragma unroll
-            for (int s = 0; s < C::NS; s++) {
-                qreg[s] = valid ? *reinterpret_cast<const i4*>(qrow + 32 * s + 16 * g) : i4{};
-            }
-            if (p.qsv != nullptr && valid) {
-                qs = p.qsv[((int64_t)b * p.Hq + h) * p.Sq + q];
-            }
+        if (p.qsv != nullptr && q < p.Sq) {
+            qs = p.qsv[((int64_t)b * p.Hq + h) * p.Sq + q];
         }
-        // s_j = t_j * qc with t_j = S_j * ks_j.  When every lane's qc is positive
-        // the row max is taken over t (one multiply per score saved); otherwise t
-        // is first scaled by qc in place and qeff = 1.
-        const float qc = qs * p.scale_log2e;
+        // s_j = t_j * qc with t_j = S_j * ks_j (S_j alone when the K scale is a
+        // single number, folded into qc).  When every lane's qc is positive the
+        // row max is taken over t; otherwise t is first scaled by qc in place
+        // and qeff = 1.
+        const float qc = KSV ? qs * p.scale_log2e : qs * p.k_scale * p.scale_log2e;
         const bool qpos = !wave_any(!(qc > 0.0f));
         const float qeff = qpos ? qc : 1.0f;
 
@@ -247,133 +218,186 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
 
-        f16x oacc[C::NDT];
+        // Q rows q0 .. q0 + 31 go by DMA into this wave's Q area, laid out like
+        // a K tile's first 32 rows; the Q^T operand of reduction step st is then
+        // a K-operand-shaped read: lane holds Q[q][32 st + 16 g .. +15]
+        const int8_t* const sQu = sQ + wave * (32 * D);
+        if (n > 0) {
+            const i32x4_t rq = uniform_rsrc(make_rsrc_v(qbase + (int64_t)q0 * p.q_ss,
+                                                        tile_bytes<32>(p.Sq - q0, (uint32_t)p.q_ss, D)));
+            const uint32_t mq = (uint32_t)__builtin_amdgcn_readfirstlane((int)reinterpret_cast<uintptr_t>(sQu));
+#pragma unroll
+            for (int j = 0; j < C::QB; j++) {
+                const int P = 64 * j + lane;
+                const int r = P / C::CH;
+                const int c = (P % C::CH) ^ i8_swz(r);
+                dma_load16(rq, (uint32_t)((int64_t)r * p.q_ss + 16 * c),
+                           (uint32_t)__builtin_amdgcn_readfirstlane((int)(mq + 1024 * j)));
+            }
+        }
+
+        // O = of * 2^(m_a - m_c) + oint (see the header); l relative to m_c
+        i16x oint[C::NDT];
+        f16x of[C::NDT];
 #pragma unroll
         for (int dt = 0; dt < C::NDT; dt++) {
-            oacc[dt] = f16x{};
+            oint[dt] = i16x{};
+            of[dt] = f16x{};
         }
-        // m_run: the scheme's exact running max; m_ref: the lagging reference
-        // O and l are kept relative to (m_ref <= m_run)
-        float m_run = -INFINITY, m_ref = -INFINITY, l_run = 0.0f;
-        f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
-        tsc[0] = f16x{};
-        tsc[1] = f16x{};
-        h8 pb[4]; // P^T operands of the four 16-key groups: integers 0..127 in fp16
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            pb[u] = h8{};
-        }
+        float m_c = -INFINITY, m_a = -INFINITY, l_c = 0.0f, beta = 0.0f;
+        bool live = false, fold = false; // wave-uniform
+        // S^T accumulators of the current tile (keys 0..31 and 32..63), turned
+        // into t = S * ks in place (as fp32 bit patterns) before the softmax
+        i16x sacc[2];
+        sacc[0] = i16x{};
+        sacc[1] = i16x{};
+        i4 pb[2]; // P^T operands of keys 0..31 and 32..63: bytes 0..127
+        pb[0] = i4{};
+        pb[1] = i4{};
         int cls_prev = 0;
 
-        // ---- staging (one group's 32 rows of K and V per pair; ks by group A)
-        i4 kreg[C::CT], vreg[C::CT];
-        uint32_t coff_k[C::CT], coff_v[C::CT];
-        int clk[C::CT], clv[C::CT];
+        // ---- DMA of tile x (K, V and the per-token K scales) into slot x % 4,
+        // issued by group A's waves
+        auto issue = [&](int x) {
+            const int key0 = (t_begin + x) * kI8BN;
+            const uint32_t slot = (uint32_t)(x & (kI8Slots - 1));
+            const i32x4_t rk = uniform_rsrc(make_rsrc_v(kbase + (int64_t)key0 * p.k_ss,
+                                                        tile_bytes<kI8BN>(Sk - key0, (uint32_t)p.k_ss, D)));
+            const i32x4_t rv = uniform_rsrc(make_rsrc_v(vbase + (int64_t)key0 * p.v_ss,
+                                                        tile_bytes<kI8BN>(Sk - key0, (uint32_t)p.v_ss, D)));
+            const uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(kv_lds + slot * (2 * C::TILE) + (uint32_t)((wave & 3) * C::BPW * 1024)));
 #pragma unroll
-        for (int it = 0; it < C::CT; it++) {
-            const int e = gtid + it * 256;
-            const bool ok = C::HALF_TASK % 256 == 0 || e < C::HALF_TASK;
-            const int row = 32 * grp + (ok ? e / C::KCH : 0);
-            const int ch = ok ? e - (e / C::KCH) * C::KCH : 0;
-            coff_k[it] = (uint32_t)((int64_t)row * p.k_ss + 16 * ch);
-            coff_v[it] = (uint32_t)((int64_t)row * p.v_ss + 16 * ch);
-            clk[it] = ok ? row * C::LDK + 16 * ch : -1;
-            clv[it] = ok ? row * C::LDV + 16 * ch : -1;
-        }
-        float ksreg = 0.0f;
-        float vsreg[C::CT]; // VTOK: the scale of each staged V row
-        auto load_pair = [&](int x) {
-            const int tk = t_begin + x, tv = t_begin + x - 1;
-            const auto rk = make_rsrc(kbase + (int64_t)tk * kI8BN * p.k_ss,
-                                      x < n ? tile_bytes<kI8BN>(Sk - tk * kI8BN, (uint32_t)p.k_ss, D) : 0u);
-            const auto rv = make_rsrc(vbase + (int64_t)tv * kI8BN * p.v_ss,
-                                      (x >= 1 && x <= n) ? tile_bytes<kI8BN>(Sk - tv * kI8BN, (uint32_t)p.v_ss, D) : 0u);
-#pragma unroll
-            for (int it = 0; it < C::CT; it++) {
-                kreg[it] = buffer_load_i4(rk, coff_k[it]);
-                vreg[it] = buffer_load_i4(rv, coff_v[it]);
-                if constexpr (VTOK) {
-                    const int key = tv * kI8BN + 32 * grp + (gtid + it * 256) / C::KCH;
-                    vsreg[it] = (x >= 1 && x <= n && key < Sk) ? vtbase[key] : 0.0f;
-                }
+            for (int jj = 0; jj < C::BPW; jj++) {
+                dma_load16(rk, dk[jj], mk + 1024 * jj);
             }
-            if (grp == 0 && gtid < kI8BN && x < n) {
-                const int key = tk * kI8BN + gtid;
-                ksreg = (ksbase != nullptr && key < Sk) ? ksbase[key] : p.k_scale;
+#pragma unroll
+            for (int jj = 0; jj < C::BPW; jj++) {
+                dma_load16(rv, dv[jj], mk + C::TILE + 1024 * jj);
+            }
+            if (KSV && wave == 0) {
+                // the tile's 64 K scales, one dword per lane (keys past Sk read 0)
+                const int left = Sk - key0;
+                const i32x4_t rs =
+                    uniform_rsrc(make_rsrc_v(ksbase + key0, (uint32_t)(4 * (left < kI8BN ? left : kI8BN))));
+                dma_load4(rs, (uint32_t)(4 * lane), ks_lds + slot * (kI8BN * 4));
             }
         };
-        auto store_pair = [&](int x) {
-            int8_t* sK = sKs + (x & 1) * C::TILE_K;
-            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
-#pragma unroll
-            for (int it = 0; it < C::CT; it++) {
-                if (C::HALF_TASK % 256 == 0 || clk[it] >= 0) {
-                    if (x < n) {
-                        *reinterpret_cast<i4*>(&sK[clk[it]]) = kreg[it];
-                    }
-                    if (x >= 1 && x <= n) {
-                        h8 lo, hi;
-                        if constexpr (VTOK) {
-                            i8x16_to_h8x2_scaled(vreg[it], vsreg[it], lo, hi);
-                        } else {
-                            i8x16_to_h8x2(vreg[it], lo, hi);
-                        }
-                        *reinterpret_cast<h8*>(&sV[clv[it]]) = lo;
-                        *reinterpret_cast<h8*>(&sV[clv[it] + 8]) = hi;
-                    }
-                }
-            }
-            if (grp == 0 && gtid < kI8BN && x < n) {
-                sks[x & 1][gtid] = ksreg;
+        // group A: wait until at most one tile's DMAs (the one issued last) are
+        // in flight, or none
+        auto wait_dmas = [&](bool keep_one) {
+            if (!keep_one) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            } else if (KSV && wave == 0) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(DPT + 1));
+            } else {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(DPT));
             }
         };
 
-        // M(i): O^T += V(i-1)^T P(i-1)^T (fp16 MFMA, i >= 1) then S(i)^T = K(i) Q^T
-        // (int8 MFMA, i < n): one stream of MFMAs whose LDS operands are read
-        // kI8OpDepth MFMAs ahead through a register ring
-        auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+        // fold of 8 accumulators (flat index 8 u .. 8 u + 7 over [dt][e]) into
+        // O_f (the next P V MFMA of their column tile restarts the chain)
+        auto fold_slice = [&](int u) {
+#pragma unroll
+            for (int f = 8 * u; f < 8 * u + 8; f++) {
+                of[f >> 4][f & 15] = fmaf(of[f >> 4][f & 15], beta, (float)oint[f >> 4][f & 15]);
+            }
+        };
+        // dequantisation of 4 scores in place (group u: keys 32 (u / 4) + 8 (u %
+        // 4) + 4 g .. +3)
+        auto dequant_group = [&](int u, const float* ksl) {
+            const int kt = u >> 2, r4 = u & 3;
+            if constexpr (KSV) {
+                const f4 ks = *reinterpret_cast<const f4*>(&ksl[32 * kt + 8 * r4 + 4 * g]);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    sacc[kt][4 * r4 + e] = __float_as_int((float)sacc[kt][4 * r4 + e] * ks[e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    sacc[kt][4 * r4 + e] = __float_as_int((float)sacc[kt][4 * r4 + e]);
+                }
+            }
+        };
+
+        // M(i): S(i)^T = K(i) Q^T (i < n), then O^T += V(i-1)^T P(i-1)^T (i >= 1):
+        // one stream of MFMAs whose LDS operands are read kI8OpDepth MFMAs
+        // ahead.  The fold (when the previous softmax moved a row max) rides on
+        // the Q K^T MFMAs and the first P V MFMA of each column tile then
+        // restarts its int32 chain; the dequantisation of S(i) rides on the P V
+        // MFMAs.
+        auto mfma_stream = [&](auto do_pv_c, auto do_s_c, auto fold_c, int i) {
             constexpr bool DO_PV = decltype(do_pv_c)::value;
             constexpr bool DO_S = decltype(do_s_c)::value;
-            constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
-            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
-            constexpr int T = NPV + NSK;
+            constexpr bool FOLD = decltype(fold_c)::value;
+            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (st, kt)
+            constexpr int NPV = DO_PV ? 2 * C::NDT : 0; // (kt, dt)
+            constexpr int T = NSK + NPV;
             constexpr int DEPTH = T < kI8OpDepth ? T : kI8OpDepth;
-            const int j16 = lane & 15;
-            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
-                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-            const int8_t* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 16 * g;
+            constexpr int GPS = NPV > 0 ? 8 / NPV : 0; // dequant groups per P V MFMA
+            const int8_t* sk = sKV + (i & (kI8Slots - 1)) * (2 * C::TILE);
+            const int8_t* sv = sKV + ((i - 1) & (kI8Slots - 1)) * (2 * C::TILE) + C::TILE;
+            const float* ksl = sks + (i & (kI8Slots - 1)) * kI8BN;
+            auto q_op = [&](int st) -> i4 { return *reinterpret_cast<const i4*>(sQu + kofs[st]); };
             auto op = [&](int j) -> i4 {
-                if (j < NPV) {
-                    const int u = j / C::NDT, dt = j % C::NDT;
-                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                    h4 lo = lds_read_tr16(base);
-                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                    return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                if (j < NSK) {
+                    const int st = j >> 1, kt = j & 1;
+                    return *reinterpret_cast<const i4*>(sk + kofs[st] + kt * 32 * D);
                 }
-                const int js = j - NPV, st = js >> 1, kt = js & 1;
-                return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
+                const int jp = j - NSK, kt = jp / C::NDT, dt = jp % C::NDT;
+                const int8_t* a = sv + vofs[dt] + kt * 32 * D;
+                const i2 lo = lds_read_tr8(a);
+                const i2 hi = lds_read_tr8(a + 16 * D);
+                return i4{lo[0], lo[1], hi[0], hi[1]};
             };
-            i16x acc0 = {}, acc1 = {};
+            if constexpr (FOLD && !DO_S) {
+#pragma unroll
+                for (int u = 0; u < 2 * C::NDT; u++) {
+                    fold_slice(u);
+                }
+            }
+            if constexpr (DO_S) {
+                sacc[0] = i16x{};
+                sacc[1] = i16x{};
+            }
             i4 ring[DEPTH > 0 ? DEPTH : 1];
 #pragma unroll
             for (int j = 0; j < DEPTH; j++) {
                 ring[j] = op(j);
             }
+            // Q^T operands: step st's read one step ahead of its first use
+            i4 qcur = DO_S ? q_op(0) : i4{}, qnext = i4{};
 #pragma unroll
             for (int j = 0; j < T; j++) {
                 const i4 a = ring[j % DEPTH];
                 if (j + DEPTH < T) {
                     ring[j % DEPTH] = op(j + DEPTH);
                 }
-                if (j < NPV) {
-                    const int u = j / C::NDT, dt = j % C::NDT;
-                    oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
+                if (j < NSK) {
+                    const int st = j >> 1, kt = j & 1;
+                    if (kt == 0 && st + 1 < C::NS) {
+                        qnext = q_op(st + 1);
+                    }
+                    sacc[kt] = mfma_32x32x32_i8(a, qcur, sacc[kt]);
+                    if (kt == 1) {
+                        qcur = qnext;
+                    }
+                    if constexpr (FOLD) {
+                        fold_slice(j); // 2 NS slots x 8 = 16 NDT accumulators
+                    }
                 } else {
-                    const int js = j - NPV, st = js >> 1;
-                    if (js & 1) {
-                        acc1 = mfma_32x32x32_i8(a, qreg[st], acc1);
+                    const int jp = j - NSK, kt = jp / C::NDT, dt = jp % C::NDT;
+                    if (FOLD && kt == 0) {
+                        oint[dt] = mfma_32x32x32_i8(a, pb[0], i16x{});
                     } else {
-                        acc0 = mfma_32x32x32_i8(a, qreg[st], acc0);
+                        oint[dt] = mfma_32x32x32_i8(a, pb[kt], oint[dt]);
+                    }
+                    if constexpr (DO_S && !SCORES) {
+#pragma unroll
+                        for (int u = GPS * jp; u < GPS * jp + GPS; u++) {
+                            dequant_group(u, ksl);
+                        }
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -388,25 +412,17 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     for (int e = 0; e < 16; e++) {
                         const int k0 = kt0 + 8 * (e >> 2) + 4 * g + (e & 3);
                         if (k0 < Sk) {
-                            srow[k0] = acc0[e];
+                            srow[k0] = sacc[0][e];
                         }
                         if (k0 + 32 < Sk) {
-                            srow[k0 + 32] = acc1[e];
+                            srow[k0 + 32] = sacc[1][e];
                         }
                     }
                 }
-            } else if constexpr (DO_S) {
-                // dequantise here: the MFMA phase is the shorter one of the two
-                const float* ksl = sks[i & 1];
+            } else if constexpr (DO_S && !DO_PV) {
 #pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    const f4 ks0 = *reinterpret_cast<const f4*>(&ksl[8 * r4 + 4 * g]);
-                    const f4 ks1 = *reinterpret_cast<const f4*>(&ksl[32 + 8 * r4 + 4 * g]);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        tsc[0][4 * r4 + e] = (float)acc0[4 * r4 + e] * ks0[e];
-                        tsc[1][4 * r4 + e] = (float)acc1[4 * r4 + e] * ks1[e];
-                    }
+                for (int u = 0; u < 8; u++) {
+                    dequant_group(u, ksl);
                 }
             }
         };
@@ -423,117 +439,130 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             using T_ = std::true_type;
             using F_ = std::false_type;
             if (do_pv && cls_now != 0) {
-                mfma_stream(T_{}, T_{}, i);
+                if (fold) {
+                    mfma_stream(T_{}, T_{}, T_{}, i);
+                } else {
+                    mfma_stream(T_{}, T_{}, F_{}, i);
+                }
             } else if (do_pv) {
-                mfma_stream(T_{}, F_{}, i);
+                if (fold) {
+                    mfma_stream(T_{}, F_{}, T_{}, i);
+                } else {
+                    mfma_stream(T_{}, F_{}, F_{}, i);
+                }
             } else if (cls_now != 0) {
-                mfma_stream(F_{}, T_{}, i);
+                mfma_stream(F_{}, T_{}, F_{}, i);
+            }
+            if (do_pv) {
+                live = true;
+                fold = false;
             }
             cls_prev = cls_now;
         };
 
-        // V(i): exact running max over the 64-key block, P as integers 0..127
-        // times the reference factor f; O and l are rescaled only when the
-        // reference moves
+        // V(i): the scheme's exact running max over the 64-key block and P as
+        // bytes 0..127; a moved maximum rescales l now and schedules the fold
+        // of O_int for the next MFMA phase
         auto phase_v = [&](int i) {
             if (SCORES || !wave_active || cls_prev == 0) {
                 return;
             }
-            f16x t[2] = {tsc[0], tsc[1]};
             if (!qpos) {
 #pragma unroll
                 for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
-                        t[kt][e] *= qc;
+                        sacc[kt][e] = __float_as_int(__int_as_float(sacc[kt][e]) * qc);
                     }
                 }
             }
             if (cls_prev == 2) {
-                const int kt0 = (t_begin + i) * kI8BN;
-                const int a = row_lo - kt0 - 4 * g;
-                const int bnd = row_hi - kt0 - 4 * g;
+                const int kt0 = (t_begin + i) * kI8BN + 4 * g;
+                const int a = row_lo - kt0;
+                const int bnd = row_hi - kt0;
 #pragma unroll
                 for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
-                        const int off = kt * 32 + 8 * (e >> 2) + (e & 3);
-                        t[kt][e] = (off < a || off > bnd) ? -INFINITY : t[kt][e];
+                        const int off = 32 * kt + 8 * (e >> 2) + (e & 3);
+                        sacc[kt][e] = (off < a || off > bnd) ? __float_as_int(-INFINITY) : sacc[kt][e];
                     }
                 }
             }
-            float mx = t[0][0];
-#pragma unroll
-            for (int e = 1; e < 16; e++) {
-                mx = fmaxf(mx, t[0][e]);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                mx = fmaxf(mx, t[1][e]);
-            }
-            mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
-            m_run = fmaxf(m_run, mx);
-            const bool move = m_run > m_ref + kI8RefThreshold; // false while m_run = -inf
-            if (wave_any(move)) {
-                const float alpha = move ? fast_exp2(m_ref - m_run) : 1.0f; // m_ref = -inf -> 0
-                if (move) {
-                    m_ref = m_run;
-                }
-                l_run *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < C::NDT; dt++) {
-                    oacc[dt] *= alpha;
-                }
-            }
-            // m_ref = -inf only while m_run = -inf (no visible key yet: every p is 0)
-            const _Float16 f16 = (_Float16)(m_ref == -INFINITY ? 1.0f : fast_exp2(m_run - m_ref));
-            const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
-            float psum = 0.0f;
+            float mx = __int_as_float(sacc[0][0]);
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    const float y = fast_exp2(fmaf(t[kt][e], qeff, c0)); // 127 p, at most 127 (+ rounding)
-                    psum += y;
-                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
+                    mx = fmaxf(mx, __int_as_float(sacc[kt][e]));
                 }
             }
-            const h8 fv = {f16, f16, f16, f16, f16, f16, f16, f16};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                pb[u] *= fv;
+            mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
+            const float m_new = fmaxf(m_c, mx);
+            if (wave_any(m_new > m_c)) {
+                // l *= 2^(m_c - m_new): 1 where the row max stayed, 0 for a first visible key
+                l_c *= (m_c == -INFINITY) ? 0.0f : fast_exp2(m_c - m_new);
+                if (live) {
+                    beta = (m_c == -INFINITY) ? 0.0f : fast_exp2(m_a - m_c); // m_a = -inf -> 0
+                    m_a = m_c;
+                    fold = true;
+                }
+                m_c = m_new;
             }
-            l_run = fmaf(psum, (float)f16, l_run);
+            const float c0 = kLog2Of127 - ((m_c == -INFINITY) ? 0.0f : m_c);
+            float psum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; kt++) {
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int e = 4 * w; e < 4 * w + 4; e++) {
+                        const float y = fast_exp2(fmaf(__int_as_float(sacc[kt][e]), qeff, c0)); // 127 p (<= 127 + rounding)
+                        psum += y;
+                        word = __builtin_amdgcn_cvt_pk_u8_f32(y, (uint32_t)(e & 3), word);
+                    }
+                    pb[kt][w] = (int)word;
+                }
+            }
+            l_c += psum;
         };
 
-        if (n > 0) {
-            load_pair(0);
-            store_pair(0);
-            load_pair(1);
+        if (grp == 0 && n > 0) {
+            issue(0);
+            if (n > 1) {
+                issue(1);
+            }
+            wait_dmas(n > 1); // Q and tile 0 landed
+        } else if (n > 0) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // Q landed
         }
         __syncthreads();
+        // Group A: M(i) in phase 2i, V(i) in phase 2i + 1; group B one phase
+        // later.  Tile x is read in phases 2x .. 2x + 3 (K in M(x), V in M(x + 1),
+        // by A then B).  Its DMAs are issued at the start of phase 2x - 4 into
+        // the slot tile x - 4 left at the end of phase 2x - 5, and group A waits
+        // for them at the end of phase 2x - 1.  Both groups pass 2n + 3 barriers.
         if (n > 0) {
             if (grp == 0) {
                 for (int i = 0; i < n; i++) {
+                    if (i + 2 < n) {
+                        issue(i + 2);
+                    }
                     phase_m(i);
                     __syncthreads();
-                    store_pair(i + 1);
-                    load_pair(i + 2);
                     phase_v(i);
+                    wait_dmas(i + 2 < n); // tile i + 1 landed
                     __syncthreads();
                 }
                 phase_m(n);
                 __syncthreads();
                 __syncthreads();
             } else {
-                store_pair(1);
-                load_pair(2);
                 __syncthreads();
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
-                    store_pair(i + 2);
-                    load_pair(i + 3);
                     phase_v(i);
                     __syncthreads();
                 }
@@ -545,13 +574,21 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         if (SCORES || !wave_active) {
             return;
         }
-        // O = O^T * v_scale / l (times the per-channel V scales of this kv head
-        // when given), through this wave's sO slot
-        const float l = pair_sum(l_run);
+        // O = (of * 2^(m_a - m_c) + oint) * v_scale / l (times the per-channel V
+        // scales of this kv head when given), through this wave's sO slot
+        const float bf = (m_c == -INFINITY) ? 0.0f : fast_exp2(m_a - m_c);
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; dt++) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                of[dt][e] = fmaf(of[dt][e], bf, (float)oint[dt][e]);
+            }
+        }
+        const float l = pair_sum(l_c);
         const float f = l > 0.0f ? p.v_scale / l : 0.0f;
         const float* vch = p.vch != nullptr ? p.vch + ((int64_t)b * p.Hkv + kvh) * D : nullptr;
         store_o_tile<D, C::LDO>(
-            oacc,
+            of,
             [&](int d0) {
                 return vch != nullptr ? f * *reinterpret_cast<const f4*>(vch + d0) : f4{f, f, f, f};
             },
@@ -566,18 +603,18 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
     }
 }
 
-template <int D, bool VTOK, bool SCORES>
+template <int D, bool KSV, bool SCORES>
 int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::string& err) {
     // persistent: as many workgroups as the device holds at once, each
     // walking its share of the n_wg row tiles
     const int64_t resident =
-        resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D, VTOK, SCORES>), kI8Threads, err);
+        resident_workgroups(reinterpret_cast<const void*>(&fa_fwd_int8<D, KSV, SCORES>), kI8Threads, err);
     if (resident <= 0) {
         return -1;
     }
     const int64_t grid = std::min(n_wg, resident);
     KernelTimerGuard timer(stream);
-    hipLaunchKernelGGL((fa_fwd_int8<D, VTOK, SCORES>), dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
+    hipLaunchKernelGGL((fa_fwd_int8<D, KSV, SCORES>), dim3((uint32_t)grid), dim3(kI8Threads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);
@@ -586,8 +623,8 @@ int launch_int8(const Int8Params& p, int64_t n_wg, hipStream_t stream, std::stri
     return 0;
 }
 
-// Kernel parameters and grid size of an INT8 launch (shared by the forward
-// and the score export).  Returns the number of row tiles, or -1 with `err`.
+} // namespace
+
 int64_t int8_params(const AttnArgs& a, Int8Params& p, std::string& err) {
     if (a.ks[2] < 0 || a.vs[2] < 0 || a.ks[2] > (1 << 24) || a.vs[2] > (1 << 24)) {
         err = "key/value seq strides must be in [0, 2^24] elements";
@@ -638,36 +675,35 @@ int64_t int8_params(const AttnArgs& a, Int8Params& p, std::string& err) {
     return n_wg;
 }
 
-} // namespace
-
 int fwd_int8(const AttnArgs& a, hipStream_t stream, std::string& err) {
     Int8Params p;
     const int64_t n_wg = int8_params(a, p, err);
     if (n_wg < 0) {
         return -1;
     }
-    switch (a.D) {
-    case 64:
-        return p.vtok ? launch_int8<64, true, false>(p, n_wg, stream, err)
-                      : launch_int8<64, false, false>(p, n_wg, stream, err);
-    case 128:
-        return p.vtok ? launch_int8<128, true, false>(p, n_wg, stream, err)
-                      : launch_int8<128, false, false>(p, n_wg, stream, err);
-    default: break;
+    if (a.D == 64 && p.vtok == nullptr) {
+        return p.ksv != nullptr ? launch_int8<64, true, false>(p, n_wg, stream, err)
+                                : launch_int8<64, false, false>(p, n_wg, stream, err);
+    }
+    if (a.D == 64 || a.D == 128) {
+        return launch_int8_f16pv(p, a.D, false, n_wg, stream, err);
     }
     err = "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)";
     return -1;
 }
 
 int int8_scores(const AttnArgs& in, int32_t* scores, hipStream_t stream, std::string& err) {
-    // the production kernel's SCORES instantiation: its K tiles, LDS layout,
-    // operand ring and MFMAs, with V staged from K and no output
+    // the production kernel's SCORES instantiation for this head dim: its K
+    // tiles, LDS layout, operand ring and MFMAs, with V staged from K and no
+    // output
     AttnArgs a = in;
     a.v = a.k;
     a.vs[0] = a.ks[0], a.vs[1] = a.ks[1], a.vs[2] = a.ks[2];
     a.o = nullptr;
     a.causal = 0;
     a.window = 0;
+    a.k_scale_vec = nullptr;
+    a.v_token = nullptr;
     Int8Params p;
     const int64_t n_wg = int8_params(a, p, err);
     if (n_wg < 0) {
@@ -676,7 +712,7 @@ int int8_scores(const AttnArgs& in, int32_t* scores, hipStream_t stream, std::st
     p.scores = scores;
     switch (a.D) {
     case 64: return launch_int8<64, false, true>(p, n_wg, stream, err);
-    case 128: return launch_int8<128, false, true>(p, n_wg, stream, err);
+    case 128: return launch_int8_f16pv(p, 128, true, n_wg, stream, err);
     default: break;
     }
     err = "unsupported head_dim (only 64 and 128 are compiled in for the int8 kernel)";

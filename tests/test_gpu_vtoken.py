@@ -2,8 +2,13 @@
 reference lists a per-token V scale as missing, FEATURES.md:191, :201-202).
 
 * Exact rows: per-token scales in {1, 2, 4} on V values in [-31, 31] dequantise
-  to exact integers, so the kernel must give bit for bit what the plain INT8
-  kernel gives on the pre-multiplied V.
+  to exact integers, so the kernel must give what the plain INT8 kernel gives
+  on the pre-multiplied V: the same scores, maxima and quantised P.  The P V
+  sums differ only by this kernel's rounding of each pq * 2^(m - m_ref) to
+  fp16 (relative 2^-11 per product, <= 2^-11 * max|v| on the output; the
+  plain kernel sums each block in exact int32), so they must agree to 1e-3
+  of the V range here, while a misindexed per-token scale (1 vs 4) would be
+  off by a sizeable fraction of it.
 * Real scales: within 1e-2 max-abs of the oracle's kernel-exact emulation
   (oracle.attention_int8(..., v_token=...)).
 * End to end: flash_attn_int8qk_quantized(v_per_token=True) against the
@@ -60,7 +65,7 @@ def _run(qi, ki, vi, qs, ks, causal, window, v_token=None):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_vtoken_exact_rows_bit_identical(gpu, case):
+def test_vtoken_exact_rows_match_plain_kernel(gpu, case):
     name, b, hq, hkv, sq, sk, d, causal, window, ptok, strided = case
     log(f"vtoken exact {name}")
     rng = np.random.default_rng(71)
@@ -72,9 +77,15 @@ def test_vtoken_exact_rows_bit_identical(gpu, case):
     qs, ks = _scales(case, rng)
     dq, dk = torch.from_numpy(qi).cuda(), torch.from_numpy(ki).cuda()
     a = _run(dq, dk, _device_v(w, strided), qs, ks, causal, window, v_token=vs)
-    ref = _run(dq, dk, _device_v(v_full, strided), qs, ks, causal, window)
+    plain = _run(dq, dk, _device_v(v_full, strided), qs, ks, causal, window)
     assert torch.isfinite(a.float()).all(), name
-    assert torch.equal(a.view(torch.int16), ref.view(torch.int16)), name
+    got = a.float().cpu().numpy()
+    ref = plain.float().cpu().numpy()
+    # outputs are in int8 units (v_scale 1): bound by 1e-3 of the V range
+    bound = 1e-3 * float(np.abs(v_full).max())
+    mx = float(np.abs(got - ref).max())
+    log(f"  max |vtoken - plain| = {mx:.3e} (bound {bound:.3e})")
+    assert mx <= bound, (name, mx, bound)
 
 
 @pytest.mark.gpu

@@ -24,6 +24,7 @@ LDS_LIMIT = 160 * 1024
 WAVES_PER_SIMD = {
     "fa_fwd_f16_pp": 2,
     "fa_fwd_int8": 2,
+    "fa_fwd_int8_f16pv": 2,
     "fa_fwd_f16_kpair": 2,
     "fa_fwd_f16_dpair": 2,
     "fa_fwd_f16_decode": 1,
@@ -61,7 +62,7 @@ def test_occupancy_fits_the_workgroup(kernels):
         if need is not None:
             assert k["waves_per_simd"] >= need, (k["kernel"], k["waves_per_simd"], need)
             checked += 1
-    # pp 4, kpair 4, dpair 8, decode 3, int8 4 (+ 2 score-export instantiations)
+    # pp 4, kpair 4, dpair 8, decode 3, int8 3 + int8_f16pv 3 (+ 2 score-export instantiations)
     assert checked >= 4 + 4 + 3 + 5 + 3 + 4
 
 
@@ -79,8 +80,11 @@ def test_every_dispatched_head_dim_is_compiled(kernels):
         assert has("fa_fwd_f16_dpair", d), d
     for d in (32, 64, 128):
         assert has("fa_fwd_f16_decode", d), d
+    # INT8: head_dim 64 with both GEMMs on int8 MFMA, 128 (and the per-token V
+    # scale) with P V on fp16 MFMA
+    assert has("fa_fwd_int8", 64)
     for d in (64, 128):
-        assert has("fa_fwd_int8", d), d
+        assert has("fa_fwd_int8_f16pv", d), d
     for frag in ("rope_rotate_rows", "fa_decode_combine", "quant_rows_kernel", "col_max_kernel",
                  "quant_cols_kernel"):
         assert any(frag in n for n in names), frag
