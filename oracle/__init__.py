@@ -19,7 +19,6 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
-REF_LIB_PATH = HERE / "_ref" / "librdnattention_ref.so"
 
 _lib = None
 
