@@ -161,35 +161,45 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             const _Float16* qb = p.q + b * p.q_sb + (int64_t)(kvh * p.ratio + sub * p.G) * p.q_sh;
             // chunk c of this thread: (head j, row r, 16-byte column ch), ch
             // fastest; row r of head j is row r % 32 of wave j + G * (r / 32).
+            // A tile holds rows_per_wg = 256 / G rows of each of G heads, G in
+            // {1, 2, 4}: head and row are a shift and a mask of the slot row
+            // (a division by rows_per_wg cost ~30 instructions per chunk).
             // Recomputed from an opaque copy of the thread id at each use so
             // that no index stays live across the loads' latency.
+            const uint32_t rsh = 8u - (uint32_t)(p.G >> 1); // log2 rows_per_wg
             struct Chunk {
-                int j, r, ch;
+                uint32_t j, r, ch;
             };
-            auto chunk = [&](int t, int c) {
-                const int idx = t + kPPThreads * c;
-                const int rj = idx / C::KCH;
-                const int j = rj / p.rows_per_wg;
-                return Chunk{j, rj - j * p.rows_per_wg, idx % C::KCH};
+            auto chunk = [&](uint32_t t, int c) {
+                const uint32_t idx = t + kPPThreads * c;
+                const uint32_t rj = idx / C::KCH;
+                return Chunk{rj >> rsh, rj & ((1u << rsh) - 1u), idx - rj * C::KCH};
             };
-            auto src_row = [&](const Chunk& k) { return wg_q0 + k.r < p.Sq ? wg_q0 + k.r : 0; };
+            auto src_row = [&](const Chunk& k) { return wg_q0 + (int)k.r < p.Sq ? (uint32_t)wg_q0 + k.r : 0u; };
             h8 x[C::QCT];
-            int t = tid;
+            f4 cs[C::QCT], sn[C::QCT];
+            uint32_t t = tid;
             asm volatile("" : "+v"(t));
-#pragma unroll
-            for (int c = 0; c < C::QCT; c++) {
-                const Chunk k = chunk(t, c);
-                x[c] = *reinterpret_cast<const h8*>(qb + k.j * p.q_sh + (int64_t)src_row(k) * p.q_ss + 8 * k.ch);
-            }
+            // The table loads are issued first, so that they and the Q loads
+            // are in flight together: issued after the Q loads, they waited
+            // for all of them (the conversions that both the rotation and the
+            // plain scaling start with were hoisted above the branch).
             if (p.rope_q) {
-                f4 cs[C::QCT], sn[C::QCT];
 #pragma unroll
                 for (int c = 0; c < C::QCT; c++) {
                     const Chunk k = chunk(t, c);
-                    const int64_t off = (int64_t)src_row(k) * (D / 2) + 4 * k.ch;
+                    const uint64_t off = (uint64_t)src_row(k) * (D / 2) + 4 * k.ch;
                     cs[c] = *reinterpret_cast<const f4*>(p.rot_cos + off);
                     sn[c] = *reinterpret_cast<const f4*>(p.rot_sin + off);
                 }
+            }
+#pragma unroll
+            for (int c = 0; c < C::QCT; c++) {
+                const Chunk k = chunk(t, c);
+                x[c] = *reinterpret_cast<const h8*>(qb + (int64_t)k.j * p.q_sh + (int64_t)src_row(k) * p.q_ss +
+                                                    8 * k.ch);
+            }
+            if (p.rope_q) {
 #pragma unroll
                 for (int c = 0; c < C::QCT; c++) {
                     x[c] = PRE ? rope8_cs_mul(x[c], cs[c], sn[c], p.qmul) : rope8_cs(x[c], cs[c], sn[c]);
@@ -205,8 +215,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
 #pragma unroll
             for (int c = 0; c < C::QCT; c++) {
                 const Chunk k = chunk(t, c);
-                const int dst = ((k.j + p.G * (k.r >> 5)) * 32 + (k.r & 31)) * C::LDQ + 8 * k.ch;
-                *reinterpret_cast<h8*>(&sQ[dst]) = wg_q0 + k.r < p.Sq ? (neg ? -x[c] : x[c]) : h8{};
+                const uint32_t dst = ((k.j + p.G * (k.r >> 5)) * 32 + (k.r & 31)) * C::LDQ + 8 * k.ch;
+                *reinterpret_cast<h8*>(&sQ[dst]) = wg_q0 + (int)k.r < p.Sq ? (neg ? -x[c] : x[c]) : h8{};
             }
         };
         auto read_q = [&]() {

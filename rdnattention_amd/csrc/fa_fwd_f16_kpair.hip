@@ -228,14 +228,79 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         if (n > 0) {
             load_pair(0);
         }
+        // Q^T is staged through the K slots, which are free until the first
+        // K/V tile is stored.  Loaded in the operand layout, each lane would
+        // read 16 B of its own row, every load instruction touching 32 rows,
+        // and the table loads came in chunks to bound the registers they
+        // hold: one round trip per chunk.  Here all 512 threads load the row
+        // tile's 128 rows (4 pairs x 32) row-contiguously, KCH lanes per row,
+        // with all loads of a thread in flight together, rotate and scale
+        // them, and write them at the K rows' stride; each wave then reads
+        // its pair's 32 rows with the K operand's conflict-free b128 reads.
         h8 qreg[C::NS];
         {
-            const bool valid = q < p.Sq;
-            const int qr = valid ? q : 0;
-            const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-            load_q_operand<C::NS, 2>(qreg, qbase + (int64_t)qr * p.q_ss, p.rot_cos + (int64_t)qr * (D / 2),
-                                     p.rot_sin + (int64_t)qr * (D / 2), g, valid, p.rope_q != 0, p.q_sign < 0.0f,
-                                     PRE ? p.qmul : 0.0f);
+            constexpr int QCT = 4 * 32 * C::KCH / kKPThreads; // chunks per thread
+            static_assert(QCT * kKPThreads == 4 * 32 * C::KCH && 4 * 32 <= 2 * kKPBN, "Q chunks, Q in the K slots");
+            const int hq0 = kvh * p.ratio + sub * p.G;
+            const int gsh = p.G >> 1; // log2 G, G in {1, 2, 4}
+            // chunk c of this thread: slot row rj (pair rj / 32), column chunk
+            // ch; pair j holds head hq0 + j % G, rows (j / G) * 32 of the tile.
+            // Recomputed from an opaque copy of the thread id at each use so
+            // that no index stays live across the loads' latency.
+            struct Chunk {
+                int rj, ch, qr;
+            };
+            auto chunk = [&](int t, int c) {
+                const int idx = t + kKPThreads * c;
+                const int rj = idx / C::KCH;
+                const int j = rj >> 5;
+                return Chunk{rj, idx - rj * C::KCH, wg_q0 + ((j >> gsh) << 5) + (rj & 31)};
+            };
+            auto head_of = [&](const Chunk& k) { return hq0 + ((k.rj >> 5) & (p.G - 1)); };
+            const _Float16* qb = p.q + b * p.q_sb;
+            int t = tid;
+            asm volatile("" : "+v"(t));
+            h8 x[QCT];
+#pragma unroll
+            for (int c = 0; c < QCT; c++) {
+                const Chunk k = chunk(t, c);
+                const int src = k.qr < p.Sq ? k.qr : 0;
+                x[c] = *reinterpret_cast<const h8*>(qb + head_of(k) * p.q_sh + (int64_t)src * p.q_ss + 8 * k.ch);
+            }
+            if (p.rope_q) {
+                f4 cs[QCT], sn[QCT];
+#pragma unroll
+                for (int c = 0; c < QCT; c++) {
+                    const Chunk k = chunk(t, c);
+                    const int64_t off = (int64_t)(k.qr < p.Sq ? k.qr : 0) * (D / 2) + 4 * k.ch;
+                    cs[c] = *reinterpret_cast<const f4*>(p.rot_cos + off);
+                    sn[c] = *reinterpret_cast<const f4*>(p.rot_sin + off);
+                }
+#pragma unroll
+                for (int c = 0; c < QCT; c++) {
+                    x[c] = PRE ? rope8_cs_mul(x[c], cs[c], sn[c], p.qmul) : rope8_cs(x[c], cs[c], sn[c]);
+                }
+            } else if constexpr (PRE) {
+#pragma unroll
+                for (int c = 0; c < QCT; c++) {
+                    x[c] = scale8(x[c], p.qmul);
+                }
+            }
+            const bool neg = !PRE && p.q_sign < 0.0f; // PRE: the sign is in qmul
+            asm volatile("" : "+v"(t));
+#pragma unroll
+            for (int c = 0; c < QCT; c++) {
+                const Chunk k = chunk(t, c);
+                *reinterpret_cast<h8*>(&sKs[k.rj * C::LDK + 8 * k.ch]) =
+                    k.qr < p.Sq ? (neg ? -x[c] : x[c]) : h8{};
+            }
+            __syncthreads();
+            const _Float16* src = sKs + (pair * 32 + l32) * C::LDK + 8 * g;
+#pragma unroll
+            for (int st = 0; st < C::NS; st++) {
+                qreg[st] = *reinterpret_cast<const h8*>(src + 16 * st);
+            }
+            __syncthreads(); // every wave holds its Q^T before the K slots are overwritten
         }
 
         f16x oacc[NDT];
@@ -338,9 +403,13 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             if (cls_now != 0) {
                 if (cls_now == 2) {
                     // own key e: kt0 + 32 HALF + 8 (e / 4) + 4 g + e % 4
-                    const int kt0 = walk(i) * kKPBN + 32 * HALF;
-                    const int a = row_lo - kt0 - 4 * g;
-                    const int bnd = row_hi - kt0 - 4 * g;
+                    // (4 g from an opaque copy of the lane id: a register
+                    // holding it across the row tile is one too many at D = 256)
+                    int lane_m = lane;
+                    asm volatile("" : "+v"(lane_m));
+                    const int kt0 = walk(i) * kKPBN + 32 * HALF + ((lane_m >> 5) << 2);
+                    const int a = row_lo - kt0;
+                    const int bnd = row_hi - kt0;
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const int off = 8 * (e >> 2) + (e & 3);

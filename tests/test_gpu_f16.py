@@ -376,6 +376,10 @@ PERSISTENT_CASES = [
     ("d64_mha_window", 2, 16, 16, 3000, 64, False, 500, False),         # 32 x 12
     ("d32_gqa2_dense", 4, 16, 8, 2100, 32, False, -1, False),           # 32 x 17
     ("d128_mqa_causal", 1, 16, 1, 2500, 128, True, -1, True),           # 4 x 40
+    # the wave-pair kernel (D 160-256), one workgroup per CU
+    ("d256_mha_window_rope", 1, 16, 16, 3000, 256, False, 1000, True),  # 16 x 24
+    ("d224_gqa2_causal", 2, 16, 8, 2100, 224, True, -1, False),         # 16 x 33
+    ("d160_gqa4_window", 1, 16, 4, 2600, 160, True, 700, True),         # 4 x 82
 ]
 
 
