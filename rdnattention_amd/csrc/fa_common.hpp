@@ -201,6 +201,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_records, 0x00020000);
 }
 
+// make_rsrc of wave-uniform values that the compiler may hold in vector
+// registers (a phi behind a lane-dependent branch): it would otherwise wrap
+// every load through the descriptor in a loop over its distinct values.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_uniform(uint64_t base, uint32_t num_records) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)base);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(base >> 32));
+    return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)num_records));
+}
+
 __device__ __forceinline__ h8 buffer_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
     u4 x = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);

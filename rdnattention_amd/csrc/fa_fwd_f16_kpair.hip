@@ -191,10 +191,8 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         auto load_pair = [&](int x) {
             const bool k_ok = x < n, v_ok = x >= 1 && x <= n;
             const int tk = k_ok ? walk(x) : 0, tv = v_ok ? walk(x - 1) : 0;
-            const auto rk = make_rsrc(reinterpret_cast<const void*>(k_addr),
-                                      k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
-            const auto rv = make_rsrc(reinterpret_cast<const void*>(v_addr),
-                                      v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
+            const auto rk = make_rsrc_uniform(k_addr, k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
+            const auto rv = make_rsrc_uniform(v_addr, v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
             // K(x + 1) is tile t_begin after the wrap at x + 1 + off = n;
             // V(x) likewise after the wrap at x + off = n
             k_addr += k_step - (x + 1 + off == n ? (uint64_t)n * k_step : 0);
