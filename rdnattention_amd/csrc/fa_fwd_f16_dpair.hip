@@ -209,7 +209,7 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
         const bool valid = q < p.Sq;
         const int qr = valid ? q : 0;
         const _Float16* qbase = p.q + b * p.q_sb + h * p.q_sh;
-        load_q_operand<NS, 2>(qreg, qbase + (int64_t)qr * p.q_ss + C0, p.rot_cos + (int64_t)qr * (D / 2) + C0 / 2,
+        load_q_operand<NS, 8>(qreg, qbase + (int64_t)qr * p.q_ss + C0, p.rot_cos + (int64_t)qr * (D / 2) + C0 / 2,
                               p.rot_sin + (int64_t)qr * (D / 2) + C0 / 2, g, valid, p.rope_q != 0, p.q_sign < 0.0f,
                               PRE ? p.qmul : 0.0f);
     }
