@@ -653,16 +653,9 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     name = args.workload
     wl = WORKLOADS[name]
-    host = cpu_inputs(wl) if wl.kind == "f16" else None
-    step = make_step(wl, dev, host)
-    ms_step, kernel_ms, launches, wall = time_steps(step, args.steps, args.warmup)
-    if launches != args.steps:
-        raise RuntimeError(f"kernel timer saw {launches} launches for {args.steps} steps")
-    if wl.kind == "decode":
-        value, unit = wl.io_bytes / (ms_step * 1e-3) / 1e9, "GB/s"
-    else:
-        value, unit = wl.flops / (ms_step * 1e-3) / 1e12, ("TOP/s" if wl.kind == "int8" else "TFLOP/s")
-
+    # The secondary workloads are measured first: the headline's warmup and
+    # timed steps then run at the clocks that sustained load holds (they ramp
+    # over the first ~20 ms, longer than a few warmup steps of the headline).
     secondary = {}
     if not args.no_secondary and name == DEFAULT:
         for other in SECONDARY:
@@ -692,6 +685,16 @@ def main(argv=None):
         except ra.RDNAttentionError as e:
             secondary["int8_quantized_end_to_end"] = {"error": str(e)}
         torch.cuda.empty_cache()
+
+    host = cpu_inputs(wl) if wl.kind == "f16" else None
+    step = make_step(wl, dev, host)
+    ms_step, kernel_ms, launches, wall = time_steps(step, args.steps, args.warmup)
+    if launches != args.steps:
+        raise RuntimeError(f"kernel timer saw {launches} launches for {args.steps} steps")
+    if wl.kind == "decode":
+        value, unit = wl.io_bytes / (ms_step * 1e-3) / 1e9, "GB/s"
+    else:
+        value, unit = wl.flops / (ms_step * 1e-3) / 1e12, ("TOP/s" if wl.kind == "int8" else "TFLOP/s")
 
     cpu = sdpa = parity = None
     if not args.no_cpu and host is not None:
