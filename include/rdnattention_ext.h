@@ -29,12 +29,13 @@ RDNA_API int32_t rdna_attention_forward_path(
     float scale, int32_t causal, int32_t has_rope, int32_t window_size,
     int32_t path, void* hip_stream);
 
-/* Releases the device memory the library keeps for reuse: the freed scratch
- * blocks (RoPE-rotated K copies, split-K partials, quantiser partials) its
- * per-device pools retain, up to 256 MiB per device, between calls.  Safe at
- * any time; memory still in use by enqueued work is not released.  No
- * reference counterpart (the reference allocates nothing).  Returns 0, or -3
- * with rdna_get_error() set. */
+/* Releases the device memory the library keeps for reuse: the scratch
+ * buffers (RoPE-rotated K copies, split-K partials, quantiser partials) it
+ * caches per (device, stream, use), grown to the largest call so far, and the
+ * blocks its per-device fallback pools retain (up to 256 MiB per device).
+ * Freeing a cached buffer synchronises its device (hipFree); a buffer a call
+ * is using at that moment is kept.  No reference counterpart (the reference
+ * allocates nothing).  Returns 0, or -3 with rdna_get_error() set. */
 RDNA_API int32_t rdna_scratch_trim(void);
 
 /* rdna_attention_forward() for callers that cannot allocate device memory

@@ -410,10 +410,12 @@ def attention_int8_forward_into(query, key, value, output, q_scale, k_scale, v_s
 
 
 def trim_scratch() -> None:
-    """Returns the scratch memory the library keeps for reuse on each device
-    (up to 256 MiB per device: freed RoPE-rotated K copies and split-K
-    partials) to the device, e.g. before handing memory to another
-    allocator.  An extension; the reference allocates nothing."""
+    """Returns the scratch memory the library keeps for reuse to the devices:
+    the buffers cached per (device, stream, use) for RoPE-rotated K copies,
+    split-K partials and quantiser partials (each grown to the largest call so
+    far), and the fallback pools' kept blocks; e.g. before handing memory to
+    another allocator.  Synchronises the devices.  An extension; the
+    reference allocates nothing."""
     if _lib_handle().rdna_scratch_trim() != 0:
         raise RDNAttentionError(f"trim_scratch failed: {last_error()}")
 

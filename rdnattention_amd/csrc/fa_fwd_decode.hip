@@ -468,7 +468,7 @@ int fwd_f16_splitk(const AttnArgs& a, bool rope_q, hipStream_t stream, std::stri
 
     // every partial is written by its split's workgroup before the combine
     // reads it, so the buffer needs no clearing
-    StreamScratch ws(region);
+    StreamScratch ws(ScratchUse::SplitKPartials, region);
     const size_t n_part = (size_t)n_bkv * splits * p.M;
     if (ws.alloc(splitk_partial_bytes(a, splits), stream, err) != 0) {
         return -1;

@@ -675,7 +675,7 @@ int fwd_f16(const AttnArgs& in, F16Path path, hipStream_t stream, std::string& e
         return -1;
     }
     const bool splitk = path == F16Path::SplitK || (path == F16Path::Auto && prefer_splitk(a));
-    StreamScratch krot(region);
+    StreamScratch krot(ScratchUse::RotatedK, region);
     if (a.has_rope && a.Sk > 0) {
         const size_t bytes = (size_t)a.B * a.Hkv * a.Sk * a.D * sizeof(_Float16);
         if (krot.alloc(bytes, stream, err) != 0 || rope_rotate_k(a, krot.ptr, stream, err) != 0) {

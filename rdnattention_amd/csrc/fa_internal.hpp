@@ -25,18 +25,31 @@ constexpr size_t region_bytes(size_t bytes) {
     return (bytes + 255) / 256 * 256;
 }
 
-// Scratch memory for one call.  Without a region: allocated with
-// hipMallocFromPoolAsync (hipMallocAsync under graph capture) on the caller's
-// stream and released with hipFreeAsync on the same stream when the object
-// goes out of scope, i.e. after every kernel that uses it has been enqueued;
-// safe across concurrent streams and under graph capture.  With a region:
-// carved from it, nothing allocated or freed (the caller has checked that it
-// fits).
+// What a scratch buffer holds; calls keep one cached buffer per (device,
+// stream, purpose), so buffers of one call never alias.
+enum class ScratchUse : int { RotatedK = 0, SplitKPartials = 1, QuantPartials = 2 };
+
+// Scratch memory for one call.  Without a region: the buffer cached for
+// (device, stream, use), allocated with hipMalloc when it first is needed or
+// must grow and reused by every later call on that stream; the call's first
+// use waits (on the GPU, hipStreamWaitEvent) for the event recorded after the
+// buffer's previous use, so a stream handle that names a new stream is
+// ordered too.  No host synchronisation in the steady state: the per-call
+// hipMallocFromPoolAsync / hipFreeAsync pair this replaces held the host until
+// the GPU had caught up, so host launch overhead fell between the steps.
+// Under graph capture, hipMallocAsync (a memory node the graph owns).  A
+// second host thread that finds the buffer in use takes a pool allocation.
+// With a region: carved from it, nothing allocated or freed (the caller has
+// checked that it fits).
 struct StreamScratch {
     void* ptr = nullptr;
     hipStream_t stream = nullptr;
     ScratchRegion* region = nullptr;
-    explicit StreamScratch(ScratchRegion* r = nullptr) : region(r) {}
+    ScratchUse use;
+    bool cached = false; // ptr is the (device, stream, use) cache entry's buffer
+    bool pooled = false; // ptr came from hipMallocFromPoolAsync / hipMallocAsync
+    int device = 0;
+    explicit StreamScratch(ScratchUse u, ScratchRegion* r = nullptr) : region(r), use(u) {}
     int alloc(size_t bytes, hipStream_t s, std::string& err);
     StreamScratch(const StreamScratch&) = delete;
     StreamScratch& operator=(const StreamScratch&) = delete;
@@ -48,8 +61,9 @@ struct StreamScratch {
 // up to 2^25 (a 4 x 8 x 4096 x 128 K is 2^24) together with split-K partials.
 constexpr size_t kNoAllocBytes = size_t(64) << 20;
 
-// Returns the freed scratch blocks the library's per-device pools keep for
-// reuse to the devices (hipMemPoolTrimTo 0).  0, or -1 with `err`.
+// Frees the cached per-stream scratch buffers that no call is using (hipFree
+// synchronises the device) and returns the blocks the per-device pools keep
+// to the devices (hipMemPoolTrimTo 0).  0, or -1 with `err`.
 int scratch_trim(std::string& err);
 
 // The no-allocation entry point's region on the current device: the

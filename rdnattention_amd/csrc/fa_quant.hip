@@ -279,7 +279,7 @@ int launch_cols(const QuantArgs& a, hipStream_t stream, std::string& err) {
     const int64_t want = std::max<int64_t>(1, 1024 / std::max<int64_t>(1, n_bh));
     int rows_per_chunk = (int)std::max<int64_t>(64, ((int64_t)a.S + want - 1) / want);
     const int n_chunks = (a.S + rows_per_chunk - 1) / rows_per_chunk;
-    StreamScratch part;
+    StreamScratch part(ScratchUse::QuantPartials);
     if (part.alloc((size_t)n_bh * n_chunks * a.D * sizeof(float), stream, err) != 0) {
         return -1;
     }

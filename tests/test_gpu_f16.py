@@ -417,3 +417,53 @@ def test_scratch_trim_between_calls(gpu, oracle_lib):
     rdnattention.trim_scratch()
     assert torch.equal(a, b)
     assert_f16_parity(a.float().cpu().numpy(), reference_f16(q, k, v, True, -1, cos, sin), "trim")
+
+
+@pytest.mark.gpu
+def test_cached_scratch_two_streams_and_growth(gpu, oracle_lib):
+    """The RoPE-rotated K scratch is one cached buffer per (device, stream):
+    calls on two streams in flight together, and a call that grows a stream's
+    buffer between two smaller ones, give the bits of the same calls made one
+    at a time."""
+    import rdnattention
+
+    shapes = [(1, 8, 2, 300, 128, True), (2, 8, 4, 900, 64, False), (1, 4, 1, 1500, 128, True)]
+    cases = []
+    for i, (b, hq, hkv, s, d, causal) in enumerate(shapes):
+        q, k, v = seeded_inputs(40 + i, b, hq, hkv, s, s, d)
+        cos, sin = oracle.rope_tables(s, d)
+        cases.append((q.to(gpu), k.to(gpu), v.to(gpu), torch.from_numpy(cos).to(gpu),
+                      torch.from_numpy(sin).to(gpu), causal))
+
+    def run(c):
+        q, k, v, cd, sd, causal = c
+        return rdnattention.flash_attn(q, k, v, is_causal=causal, rot_cos=cd, rot_sin=sd)
+
+    log("[cached scratch] one at a time")
+    refs = []
+    for c in cases:
+        refs.append(run(c))
+        torch.cuda.synchronize()
+    rdnattention.trim_scratch()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    log("[cached scratch] two streams, growing buffers")
+    outs = []
+    for _ in range(3):
+        with torch.cuda.stream(s1):
+            outs.append((0, run(cases[0])))
+            outs.append((2, run(cases[2])))  # grows s1's buffer
+            outs.append((0, run(cases[0])))
+        with torch.cuda.stream(s2):
+            outs.append((1, run(cases[1])))
+            outs.append((2, run(cases[2])))
+    torch.cuda.synchronize()
+    for i, o in outs:
+        assert torch.equal(o, refs[i]), i
+    for i, c in enumerate(cases):
+        q, k, v, cd, sd, causal = c
+        assert_f16_parity(refs[i].float().cpu().numpy(),
+                          reference_f16(q.cpu(), k.cpu(), v.cpu(), causal, -1, cd.cpu().numpy(), sd.cpu().numpy()),
+                          f"cached scratch {i}")
+    rdnattention.trim_scratch()
