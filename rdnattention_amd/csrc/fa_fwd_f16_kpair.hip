@@ -74,10 +74,12 @@ struct KPCfg {
     static constexpr int XP_BYTES = kKPWaves * 2 * 64 * 16;
     static constexpr int XS_BYTES = kKPWaves * 64 * 4;
     static constexpr int SMEM_BYTES = KV_BYTES + XP_BYTES + 2 * XS_BYTES;
-    // MFMA operands in flight, and a persistent grid: above D = 192 the
-    // persistent loop's live state, and at D = 256 also the deeper ring, do
-    // not fit 256 registers
-    static constexpr int OP_DEPTH = D <= 224 ? 4 : 2;
+    // MFMA operands in flight (a 4-deep ring does not fit 256 registers at
+    // D = 256), and a persistent grid up to D = 192: at D = 224 and 256 it
+    // fits the registers but measured slower, since the static assignment
+    // loses the dispatch order that keeps concurrent row tiles on shared key
+    // tiles
+    static constexpr int OP_DEPTH = D <= 224 ? 4 : 3;
     static constexpr bool PERSIST = D <= 192;
     static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
     static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
