@@ -31,8 +31,9 @@ RDNA_API int32_t rdna_attention_forward_path(
 
 /* Releases the device memory the library keeps for reuse: the scratch
  * buffers (RoPE-rotated K copies, split-K partials, quantiser partials) it
- * caches per (device, stream, use), grown to the largest call so far, and the
- * blocks its per-device fallback pools retain (up to 256 MiB per device).
+ * caches per (device, stream, use), grown to the largest call so far (at most
+ * 256 MiB each), and the blocks its per-device fallback pools retain (up to
+ * 256 MiB per device).
  * Freeing a cached buffer synchronises its device (hipFree); a buffer a call
  * is using at that moment is kept.  No reference counterpart (the reference
  * allocates nothing).  Returns 0, or -3 with rdna_get_error() set. */

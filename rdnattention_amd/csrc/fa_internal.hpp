@@ -34,7 +34,8 @@ enum class ScratchUse : int { RotatedK = 0, SplitKPartials = 1, QuantPartials = 
 // must grow and reused by every later call on that stream; the call's first
 // use waits (on the GPU, hipStreamWaitEvent) for the event recorded after the
 // buffer's previous use, so a stream handle that names a new stream is
-// ordered too.  No host synchronisation in the steady state: the per-call
+// ordered too; buffers above 256 MiB are not cached but taken from a pool per
+// call.  No host synchronisation in the steady state: the per-call
 // hipMallocFromPoolAsync / hipFreeAsync pair this replaces held the host until
 // the GPU had caught up, so host launch overhead fell between the steps.
 // Under graph capture, hipMallocAsync (a memory node the graph owns).  A

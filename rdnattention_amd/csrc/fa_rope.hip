@@ -11,6 +11,7 @@
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
 
+#include <algorithm>
 #include <cstdint>
 #include <map>
 #include <tuple>
@@ -49,8 +50,9 @@ constexpr uint64_t kScratchRetain = 256ull << 20;
 std::mutex g_pool_mu;
 std::map<int, hipMemPool_t> g_pools; // device -> its scratch pool; guarded by g_pool_mu
 
-// One memory pool per device, created on first use, for the scratch of a
-// call that finds its stream's cached buffer held by another host thread.
+// One memory pool per device, created on first use, for scratch above the
+// cache limit and for a call that finds its stream's cached buffer held by
+// another host thread.
 // Its release threshold keeps up to kScratchRetain bytes (256 MiB) of freed
 // blocks instead of returning them to the device at each synchronisation.
 // rdna_scratch_trim() releases what the pools and the caches hold.
@@ -176,7 +178,10 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
         err = std::string("scratch allocation failed: ") + hipGetErrorString(e);
         return -1;
     }
-    {
+    // Buffers above kScratchRetain are not cached, which bounds what a stream
+    // keeps per use; calls that large run long enough that the pool
+    // allocation's host wait costs little.
+    if (bytes <= kScratchRetain) {
         std::lock_guard<std::mutex> lock(g_pool_mu);
         CachedScratch& c = g_cache[std::make_tuple(device, s, static_cast<int>(use))];
         if (!c.busy) {
@@ -192,7 +197,7 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
                         return -1;
                     }
                 }
-                const size_t want = (bytes + kCacheGranule - 1) / kCacheGranule * kCacheGranule;
+                const size_t want = std::min(kScratchRetain, (bytes + kCacheGranule - 1) / kCacheGranule * kCacheGranule);
                 e = hipMalloc(&c.ptr, want);
                 if (e != hipSuccess) {
                     c.ptr = nullptr;
@@ -218,7 +223,8 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
             return 0;
         }
     }
-    // the cached buffer is held by another host thread's call on this stream
+    // above the cache limit, or the cached buffer is held by another host
+    // thread's call on this stream
     hipMemPool_t pool = nullptr;
     if (scratch_pool(pool, err) != 0) {
         return -1;
