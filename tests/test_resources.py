@@ -12,6 +12,7 @@ choices against a VGPR cap, tests/head_dim_resources.py):
 * every head dim the dispatchers can select is compiled in.
 """
 import json
+import os
 import re
 
 import pytest
@@ -88,3 +89,36 @@ def test_every_dispatched_head_dim_is_compiled(kernels):
     for frag in ("rope_rotate_rows", "fa_decode_combine", "quant_rows_kernel", "col_max_kernel",
                  "quant_cols_kernel"):
         assert any(frag in n for n in names), frag
+
+
+ATTENTION_SOURCES = ["fa_fwd_f16.hip", "fa_fwd_f16_kpair.hip", "fa_fwd_f16_dpair.hip", "fa_fwd_int8.hip",
+                     "fa_fwd_int8_f16pv.hip", "fa_fwd_decode.hip"]
+
+
+def test_no_waterfall_loops(tmp_path):
+    """A buffer descriptor that the compiler holds in vector registers (a
+    wave-uniform value it cannot prove uniform) gets a loop around every load
+    through it, once per distinct descriptor: v_readfirstlane of each dword,
+    two v_cmp_eq_u64, an exec save and restore and a branch.  The D = 256
+    wave-pair kernel had eight per key tile, 5 % of its time.  The attention
+    kernels' device assembly, built with the library's flags, has none."""
+    import shutil
+    import subprocess
+
+    if not shutil.which(_build.HIPCC) and not os.path.exists(_build.HIPCC):
+        pytest.skip("hipcc not found")
+    procs = []
+    for src in ATTENTION_SOURCES:
+        extra = ["-fno-honor-nans"] if src in _build.NO_NAN_SOURCES else []
+        out = tmp_path / (src + ".s")
+        cmd = [_build.HIPCC, "-x", "hip", "--offload-arch=gfx950", *_build.COMMON, *_build.DEVICE_FLAGS, *extra,
+               "--cuda-device-only", "-S", str(_build.CSRC / src), "-o", str(out)]
+        procs.append((src, out, subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE)))
+    found = {}
+    for src, out, p in procs:
+        _, err = p.communicate(timeout=600)
+        assert p.returncode == 0, (src, err.decode()[-2000:])
+        n = sum(1 for line in out.read_text().splitlines() if "v_cmp_eq_u64" in line)
+        if n:
+            found[src] = n
+    assert not found, found
