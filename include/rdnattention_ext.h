@@ -32,12 +32,22 @@ RDNA_API int32_t rdna_attention_forward_path(
 /* Releases the device memory the library keeps for reuse: the scratch
  * buffers (RoPE-rotated K copies, split-K partials, quantiser partials) it
  * caches per (device, stream, use), grown to the largest call so far (at most
- * 256 MiB each), and the blocks its per-device fallback pools retain (up to
- * 256 MiB per device).
- * Freeing a cached buffer synchronises its device (hipFree); a buffer a call
- * is using at that moment is kept.  No reference counterpart (the reference
+ * 256 MiB each, at most 1 GiB per device over all streams and uses), and the
+ * free blocks of the devices' default memory pools.  A call never frees or
+ * allocates scratch on the host's time: a cached buffer large enough is
+ * reused with no allocator call; growth and eviction are stream-ordered
+ * (hipFreeAsync / hipMallocAsync).  This trim is the one synchronising path:
+ * it waits for each buffer's last use and for its device; a buffer a call is
+ * using at that moment is kept.  No reference counterpart (the reference
  * allocates nothing).  Returns 0, or -3 with rdna_get_error() set. */
 RDNA_API int32_t rdna_scratch_trim(void);
+
+/* The scratch cache of HIP device `device`: bytes it holds, buffers it holds,
+ * and the allocator calls (hipMallocAsync) the library has made for that
+ * device's scratch since it was loaded.  For tests and monitoring; no
+ * reference counterpart.  Returns 0, or -3 if an output pointer is null. */
+RDNA_API int32_t rdna_scratch_stats(int32_t device, uint64_t* cached_bytes, int64_t* entries,
+                                    int64_t* allocations);
 
 /* rdna_attention_forward() for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
@@ -101,7 +111,8 @@ RDNA_API int32_t rdna_attention_forward_int8qk_vchannel(
 
 /* rdna_attention_forward_int8qk() with a per-token V scale: V row j of each
  * (batch, kv head) is dequantised by v_token_vec[b, kv_head, j] while the
- * kernel stages it, v'_j = fp16(v_i8[j] * fp16(v_token_vec[...])), and the
+ * kernel stages it, v'_j = fp16(sat(v_i8[j] * v_token_vec[...])) (the product
+ * in fp32, saturated to +-65504, rounded once to fp16), and the
  * quantised P (the reference's pq = min(127, round(127 p))) multiplies these
  * fp16 rows: output = sum_j pq_j v'_j * v_scale / (127 l).  v_token_vec is a
  * contiguous fp32 [batch, num_kv_heads, key_seq_len] device array (4-byte

@@ -123,6 +123,9 @@ def _lib_handle():
         try:  # absent from libraries built before it existed
             lib.rdna_scratch_trim.argtypes = []
             lib.rdna_scratch_trim.restype = _I32
+            lib.rdna_scratch_stats.argtypes = [_I32, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_I64),
+                                               ctypes.POINTER(_I64)]
+            lib.rdna_scratch_stats.restype = _I32
         except AttributeError:
             pass
         lib.rdna_kernel_timer_enable.argtypes = [_I32]
@@ -413,11 +416,22 @@ def trim_scratch() -> None:
     """Returns the scratch memory the library keeps for reuse to the devices:
     the buffers cached per (device, stream, use) for RoPE-rotated K copies,
     split-K partials and quantiser partials (each grown to the largest call so
-    far), and the fallback pools' kept blocks; e.g. before handing memory to
-    another allocator.  Synchronises the devices.  An extension; the
-    reference allocates nothing."""
+    far; at most 1 GiB per device), and the free blocks of the devices'
+    default memory pools; e.g. before handing memory to another allocator.
+    Synchronises the devices.  An extension; the reference allocates nothing."""
     if _lib_handle().rdna_scratch_trim() != 0:
         raise RDNAttentionError(f"trim_scratch failed: {last_error()}")
+
+
+def scratch_stats(device: int = 0) -> dict:
+    """The scratch cache of HIP device `device`: {"cached_bytes", "entries",
+    "allocations"}, the last being the allocator calls the library has made
+    for that device's scratch since it was loaded.  An extension."""
+    nbytes, entries, allocs = ctypes.c_uint64(), _I64(), _I64()
+    if _lib_handle().rdna_scratch_stats(int(device), ctypes.byref(nbytes), ctypes.byref(entries),
+                                        ctypes.byref(allocs)) != 0:
+        raise RDNAttentionError(f"scratch_stats failed: {last_error()}")
+    return {"cached_bytes": nbytes.value, "entries": entries.value, "allocations": allocs.value}
 
 
 class KernelTimer:

@@ -275,6 +275,15 @@ RDNA_API int32_t rdna_scratch_trim(void) {
     return 0;
 }
 
+RDNA_API int32_t rdna_scratch_stats(int32_t device, uint64_t* cached_bytes, int64_t* entries,
+                                    int64_t* allocations) {
+    if (cached_bytes == nullptr || entries == nullptr || allocations == nullptr) {
+        set_error("Scratch stats failed: %s", std::string("null output pointer"));
+        return -3;
+    }
+    return rdna_amd::scratch_stats(device, *cached_bytes, *entries, *allocations);
+}
+
 RDNA_API int32_t rdna_attention_forward_path(const void* q, const void* k, const void* v, void* output,
                                              const void* rot_cos, const void* rot_sin, int64_t q_stride_b,
                                              int64_t q_stride_h, int64_t q_stride_s, int64_t k_stride_b,

@@ -22,14 +22,17 @@
 // and O_f (fp32, relative to m_a) holds everything before.  While no row
 // maximum moves, blocks accumulate in int32 with no VALU work at all; when one
 // moves, the wave folds O_int into O_f once (one conversion and one fma per
-// accumulator) and restarts the int32 chain.  Each block's sum is therefore
+// accumulator) and restarts the int32 chain; it also folds after kI8FoldTiles
+// tiles without a move, before the int32 sums could overflow.  Each block's sum is therefore
 // the reference's exact int32 sum, and its weight 2^(m_b - m_final) is applied
 // in fp32 as the reference's per-block rescale does.
 //
 // Deliberate differences, all far below the INT8 tolerance: round() is
 // round-half-to-even (v_cvt_pk_u8_f32) where the reference calls lroundf
-// (half away from zero), 127 p is evaluated as 2^(s - m' + log2 127) (at most
-// 127 plus rounding, so the min(127) never binds), s is formed as
+// (half away from zero), 127 p is evaluated as 2^(s - m' + log2 127) (kept at
+// most 127 by the exponent offset, int8_exp_offset, so the min(127) is
+// implied and a quantised P never reaches 128, which the signed int8 MFMA
+// operand would read as -128), s is formed as
 // (S * ks) * (qs * scale * log2(e)), and v_scale/127 is applied once at the end.
 //
 // Kernel structure: 8 waves in two groups of four that alternate an MFMA phase
@@ -67,7 +70,10 @@ typedef int i2 __attribute__((ext_vector_type(2)));
 
 constexpr int kI8Slots = 4;                  // K/V tile slots in LDS (DMAs run two tiles ahead)
 constexpr int kI8OpDepth = 4;                // LDS operands in flight in the MFMA phase
-constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
+// P V tiles the int32 accumulators may sum between two folds: each tile adds
+// at most 64 * 127 * 127 = 1032256 per accumulator, so 1024 tiles stay below
+// 2^30 (2080 would pass 2^31)
+constexpr int kI8FoldTiles = 1024;
 
 template <int D>
 struct I8Cfg {
@@ -246,6 +252,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         }
         float m_c = -INFINITY, m_a = -INFINITY, l_c = 0.0f, beta = 0.0f;
         bool live = false, fold = false; // wave-uniform
+        int run_tiles = 0;               // P V tiles summed in oint since its chain last restarted
         // S^T accumulators of the current tile (keys 0..31 and 32..63), turned
         // into t = S * ks in place (as fp32 bit patterns) before the softmax
         i16x sacc[2];
@@ -454,6 +461,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 mfma_stream(F_{}, T_{}, F_{}, i);
             }
             if (do_pv) {
+                run_tiles = fold ? 1 : run_tiles + 1;
                 live = true;
                 fold = false;
             }
@@ -499,7 +507,10 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
             }
             mx = pair_max(mx) * qeff; // qeff > 0: -inf stays -inf
             const float m_new = fmaxf(m_c, mx);
-            if (wave_any(m_new > m_c)) {
+            // a moved maximum folds O_int; so does a chain of kI8FoldTiles P V
+            // tiles (rows whose maximum settled early, on long key ranges),
+            // before the int32 sums could overflow
+            if (wave_any(m_new > m_c) || (live && run_tiles >= kI8FoldTiles)) {
                 // l *= 2^(m_c - m_new): 1 where the row max stayed, 0 for a first visible key
                 l_c *= (m_c == -INFINITY) ? 0.0f : fast_exp2(m_c - m_new);
                 if (live) {
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 }
                 m_c = m_new;
             }
-            const float c0 = kLog2Of127 - ((m_c == -INFINITY) ? 0.0f : m_c);
+            const float c0 = int8_exp_offset(m_c); // y <= 127: a packed 128 would read as -128
             float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
@@ -518,7 +529,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                     uint32_t word = 0;
 #pragma unroll
                     for (int e = 4 * w; e < 4 * w + 4; e++) {
-                        const float y = fast_exp2(fmaf(__int_as_float(sacc[kt][e]), qeff, c0)); // 127 p (<= 127 + rounding)
+                        const float y = fast_exp2(fmaf(__int_as_float(sacc[kt][e]), qeff, c0)); // 127 p, <= 127
                         psum += y;
                         word = __builtin_amdgcn_cvt_pk_u8_f32(y, (uint32_t)(e & 3), word);
                     }

@@ -93,7 +93,6 @@ struct I8Cfg {
 };
 
 constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
-constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
 constexpr float kI8RefThreshold = 8.0f;      // log2 units: P is scaled by at most 2^8 (127 * 256 < 65504)
 
 __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
@@ -472,7 +471,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
             }
             // m_ref = -inf only while m_run = -inf (no visible key yet: every p is 0)
             const _Float16 f16 = (_Float16)(m_ref == -INFINITY ? 1.0f : fast_exp2(m_run - m_ref));
-            const float c0 = kLog2Of127 - ((m_run == -INFINITY) ? 0.0f : m_run);
+            const float c0 = int8_exp_offset(m_run);
             float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {

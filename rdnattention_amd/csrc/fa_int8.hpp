@@ -18,6 +18,23 @@ constexpr int kI8Waves = 8;
 constexpr int kI8Threads = 64 * kI8Waves;
 constexpr int kI8BN = 64; // keys per tile = the reference's max-update block (Bc)
 
+constexpr float kLog2Of127 = 6.98868468677f; // log2(127)
+
+// c0 of the scheme's y = 127 p = 2^(s - m + log2 127), evaluated as
+// fma(t, qeff, c0) with c0 = log2(127) - m (m = the running max, 0 while it
+// is -inf).  The reference clamps pq = min(127, lroundf(127 p))
+// (src/rdna/fa2_forward_int8qk.hip:335-339); here the bound comes from c0.
+// The block maximum gives y <= 127 * 2^(e), e the rounding of m (from its
+// product) and of c0, each within ulp(m): below |m| = 2^15, e <= 2^-8 and
+// y <= 127.35 rounds to 127.  Above, c0 is lowered by |m| 2^-21 (at least
+// four ulp(m)), so y < 127 there too; those rows' scores carry less than 8
+// fractional bits in fp32 anyway.
+__device__ __forceinline__ float int8_exp_offset(float m) {
+    const float mc = m == -INFINITY ? 0.0f : m;
+    const float a = fabsf(mc);
+    return (kLog2Of127 - mc) - (a >= 32768.0f ? a * 0x1p-21f : 0.0f);
+}
+
 struct Int8Params {
     const int8_t* q;
     const int8_t* k;

@@ -29,17 +29,16 @@ constexpr size_t region_bytes(size_t bytes) {
 // stream, purpose), so buffers of one call never alias.
 enum class ScratchUse : int { RotatedK = 0, SplitKPartials = 1, QuantPartials = 2 };
 
-// Scratch memory for one call.  Without a region: the buffer cached for
-// (device, stream, use), allocated with hipMalloc when it first is needed or
-// must grow and reused by every later call on that stream; the call's first
-// use waits (on the GPU, hipStreamWaitEvent) for the event recorded after the
-// buffer's previous use, so a stream handle that names a new stream is
-// ordered too; buffers above 256 MiB are not cached but taken from a pool per
-// call.  No host synchronisation in the steady state: the per-call
-// hipMallocFromPoolAsync / hipFreeAsync pair this replaces held the host until
-// the GPU had caught up, so host launch overhead fell between the steps.
-// Under graph capture, hipMallocAsync (a memory node the graph owns).  A
-// second host thread that finds the buffer in use takes a pool allocation.
+// Scratch memory for one call (scratch.cpp).  Without a region: the buffer
+// cached for (device, stream, use); a call that finds it large enough makes
+// no allocator call, and the call's first use waits on the GPU
+// (hipStreamWaitEvent) for the event recorded after the buffer's previous
+// use.  Growth replaces the buffer with hipMallocAsync after releasing the
+// old one with hipFreeAsync in the stream's order; the cached bytes of a
+// device are capped, with idle entries evicted least recently used first;
+// buffers above 256 MiB, calls under graph capture and a second host thread
+// that finds the buffer in use take a per-call default-pool block
+// (hipMallocAsync / hipFreeAsync).  No path here waits on the host.
 // With a region: carved from it, nothing allocated or freed (the caller has
 // checked that it fits).
 struct StreamScratch {
@@ -48,7 +47,7 @@ struct StreamScratch {
     ScratchRegion* region = nullptr;
     ScratchUse use;
     bool cached = false; // ptr is the (device, stream, use) cache entry's buffer
-    bool pooled = false; // ptr came from hipMallocFromPoolAsync / hipMallocAsync
+    bool pooled = false; // ptr is a per-call hipMallocAsync block
     int device = 0;
     explicit StreamScratch(ScratchUse u, ScratchRegion* r = nullptr) : region(r), use(u) {}
     int alloc(size_t bytes, hipStream_t s, std::string& err);
@@ -62,10 +61,15 @@ struct StreamScratch {
 // up to 2^25 (a 4 x 8 x 4096 x 128 K is 2^24) together with split-K partials.
 constexpr size_t kNoAllocBytes = size_t(64) << 20;
 
-// Frees the cached per-stream scratch buffers that no call is using (hipFree
-// synchronises the device) and returns the blocks the per-device pools keep
-// to the devices (hipMemPoolTrimTo 0).  0, or -1 with `err`.
+// Frees the cached scratch buffers that no call is using (after their last
+// use has completed) and returns the default memory pools' free blocks to the
+// devices; synchronises each device that has cached scratch.  0, or -1 with
+// `err`.
 int scratch_trim(std::string& err);
+
+// Cached scratch of `device`: bytes held, buffers held, and the allocator
+// calls made for it so far (cache growth and per-call blocks).  Always 0.
+int scratch_stats(int device, uint64_t& cached_bytes, int64_t& entries, int64_t& allocations);
 
 // The no-allocation entry point's region on the current device: the
 // library's static scratch array (fa_noalloc.hip), its device address looked

@@ -310,3 +310,17 @@ def test_scratch_trim_without_pools(lib):
     """rdna_scratch_trim with no pool created yet (no HIP call made) is a no-op."""
     lib.rdna_scratch_trim.restype = ctypes.c_int32
     assert lib.rdna_scratch_trim() == 0
+
+
+def test_scratch_stats_without_device(lib):
+    """rdna_scratch_stats of a device the library never used reports nothing
+    cached and no allocator call; a null output pointer is refused with -3."""
+    lib.rdna_scratch_stats.restype = ctypes.c_int32
+    lib.rdna_scratch_stats.argtypes = [ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64),
+                                       ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]
+    nbytes, entries, allocs = ctypes.c_uint64(7), ctypes.c_int64(7), ctypes.c_int64(7)
+    assert lib.rdna_scratch_stats(0, ctypes.byref(nbytes), ctypes.byref(entries), ctypes.byref(allocs)) == 0
+    assert (nbytes.value, entries.value, allocs.value) == (0, 0, 0)
+    assert lib.rdna_scratch_stats(0, None, ctypes.byref(entries), ctypes.byref(allocs)) == -3
+    lib.rdna_get_error.restype = ctypes.c_char_p
+    assert b"null output pointer" in lib.rdna_get_error()

@@ -214,6 +214,36 @@ def test_rows_without_keys_are_zero(gpu, oracle_lib):
     assert_f16_parity(o, reference_f16(q, k, v, True, -1), "no_keys")
 
 
+# head dims of every prefill kernel family: 8-wave ping-pong (<= 128), key
+# pairs (160-256, built with -fno-honor-nans: an all-masked row must not
+# produce -inf - -inf), head-dimension pairs (288-512); GQA ratio 2
+@pytest.mark.parametrize("d", [32, 128, 160, 192, 224, 256, 320, 512])
+@pytest.mark.parametrize("mode", ["causal_sq_gt_sk", "window_misses_rows", "causal_window_gqa"])
+def test_rows_without_keys_every_kernel(gpu, oracle_lib, d, mode):
+    """Rows that see no key are written as 0, and every other row matches the
+    oracle: causal with Sq > Sk (the first Sq - Sk rows); a two-sided window
+    with Sq > Sk whose band misses the whole key range for the first rows; a
+    causal window (GQA) where Sq > Sk leaves rows without keys and the window
+    cuts the rest (several key tiles, so masked, mask-free and skipped tiles
+    all occur).  The output is pre-filled with 7 so an unwritten row fails."""
+    sq, sk, causal, window = {"causal_sq_gt_sk": (300, 100, True, -1),
+                              "window_misses_rows": (600, 100, False, 64),
+                              "causal_window_gqa": (400, 330, True, 48)}[mode]
+    hq, hkv = (4, 2) if mode == "causal_window_gqa" else (2, 2)
+    log(f"[f16 empty rows] d{d} {mode} sq{sq} sk{sk}")
+    q, k, v = seeded_inputs(31, 1, hq, hkv, sq, sk, d)
+    out = torch.full_like(q, 7.0, device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal, window) == 0
+    torch.cuda.synchronize()
+    o = out.float().cpu().numpy()
+    ref = reference_f16(q, k, v, causal, window)
+    empty = np.all(ref == 0.0, axis=(0, 1, 3))
+    n_empty = {"causal_sq_gt_sk": 200, "window_misses_rows": 468, "causal_window_gqa": 70}[mode]
+    assert int(empty.sum()) == n_empty and empty[:n_empty].all()
+    assert np.all(o[:, :, empty] == 0.0)
+    assert_f16_parity(o, ref, f"no_keys d{d} {mode}")
+
+
 @pytest.mark.parametrize("d", [128, 256, 512])
 def test_first_causal_row_exact(gpu, d):
     q, k, v = seeded_inputs(6, 1, 4, 4, 128, 128, d)

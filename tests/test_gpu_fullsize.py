@@ -137,3 +137,36 @@ def test_c3_int8_causal_gqa_pertoken(gpu, oracle_lib):
     mx, mean, rel = errors(got, ref)
     log(f"  max_abs={mx:.3e} mean_abs={mean:.3e} rel_rms={rel:.3e}")
     assert mx <= I8_MAX_ABS, f"max_abs={mx:.3e}"
+
+
+def test_c3_int8_dropin_per_tensor_v(gpu, oracle_lib):
+    """The drop-in rdna_attention_forward_int8qk at the full INT8 workload
+    size (B2 Hq32 Hkv8 S8192 D128, causal GQA), as a C-ABI caller uses it:
+    per-token Q/K scale vectors and a per-tensor V scale v_scale = amax/127,
+    so the fp16 output is in real units.  Against the kernel-exact emulation
+    at the same scales, every element."""
+    from tests.test_gpu_int8 import forward_i8
+
+    log("[full] c3 INT8 drop-in symbol, per-token Q/K, per-tensor V")
+    b, hq, hkv, s, d = 2, 32, 8, 8192, 128
+    g = torch.Generator().manual_seed(2)
+    qf = torch.randn(b, hq, s, d, generator=g).numpy()
+    kf = torch.randn(b, hkv, s, d, generator=g).numpy()
+    vf = torch.randn(b, hkv, s, d, generator=g).numpy()
+    qi, qs = oracle.quant_pertoken(qf)
+    ki, ks = oracle.quant_pertoken(kf)
+    vs = np.float32(np.abs(vf).max() / np.float32(127.0))
+    vi = np.clip(np.rint(vf / vs), -127, 127).astype(np.int8)
+    del qf, kf, vf
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    out = torch.full((b, hq, s, d), float("nan"), dtype=torch.float16, device=gpu)
+    assert forward_i8(t(qi), t(ki), t(vi), out, t(qs), t(ks), float(vs), True, -1) == 0
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    del out
+    torch.cuda.empty_cache()
+    ref = oracle.attention_int8(qi, ki, vi, qs, ks, float(vs), causal=True)
+    assert np.isfinite(got).all()
+    mx, mean, rel = errors(got, ref)
+    log(f"  max_abs={mx:.3e} mean_abs={mean:.3e} rel_rms={rel:.3e}")
+    assert mx <= I8_MAX_ABS, f"max_abs={mx:.3e}"

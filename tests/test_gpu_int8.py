@@ -265,3 +265,89 @@ def test_int8_persistent_workgroups_cover_every_tile(gpu, oracle_lib, case):
     vscale = np.repeat(vch, hq // hkv, axis=1)[:, :, None, :]
     mx, _, _ = errors(got if vchan else got * vscale, emu * vscale)
     assert mx <= I8_MAX_ABS, f"{name}: max_abs {mx:.3e}"
+
+
+def test_int8_scores_measured_workload_slice(gpu, oracle_lib):
+    """The production kernel's int32 scores at a slice of the measured INT8
+    workload (per-token quantised N(0,1) rows, one kv group: B1 Hq4 Hkv1
+    S4096 D128), bit for bit against a float64 matmul of the same int8 values
+    (exact: every partial sum is an integer below 127^2 * 128 < 2^53)."""
+    log("[int8 scores] measured-workload slice B1 Hq4 Hkv1 S4096 D128")
+    g = torch.Generator().manual_seed(2)
+    b, hq, hkv, s, d = 1, 4, 1, 4096, 128
+    qi, _ = oracle.quant_pertoken(torch.randn(b, hq, s, d, generator=g).numpy())
+    ki, _ = oracle.quant_pertoken(torch.randn(b, hkv, s, d, generator=g).numpy())
+    qd, kd = torch.from_numpy(qi).to(gpu), torch.from_numpy(ki).to(gpu)
+    got = torch.full((b, hq, s, s), -1, dtype=torch.int32, device=gpu)
+    qs, ks = qd.stride(), kd.stride()
+    rc = lib().rdna_int8_qk_scores(qd.data_ptr(), kd.data_ptr(), got.data_ptr(), qs[0], qs[1], qs[2], ks[0], ks[1],
+                                   ks[2], b, hq, hkv, s, s, d, stream_ptr())
+    assert rc == 0
+    ref = torch.matmul(qd.double(), kd.double().transpose(-1, -2).contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(got.long(), ref.long())
+    del got, ref
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_int8_long_keys_no_int32_overflow(gpu, d):
+    """150000 keys (2344 key tiles) against all-zero query rows: every score is
+    0, so the running maximum never moves after the first tile and every p is
+    1 (pq = 127).  Columns of V that are all +127 or all -127 then add
+    127 * 127 * 64 per tile to one P V accumulator, which passes 2^31 after
+    2080 tiles unless the int32 accumulation is folded into fp32 in time.
+    The output is the mean of each V column times v_scale (closed form)."""
+    log(f"[int8 long keys] d{d} Sk 150000, zero queries, constant V columns")
+    b, h, sq, sk = 1, 1, 3, 150000
+    rng = np.random.default_rng(11)
+    qi = np.zeros((b, h, sq, d), np.int8)
+    ki = rng.integers(-127, 128, (b, h, sk, d), dtype=np.int8)
+    vi = rng.integers(-127, 128, (b, h, sk, d), dtype=np.int8)
+    vi[..., : d // 4] = 127
+    vi[..., d // 4: d // 2] = -127
+    vs = 1.0 / 127.0
+    out = torch.full((b, h, sq, d), float("nan"), dtype=torch.float16, device=gpu)
+    rc = forward_i8(torch.from_numpy(qi).to(gpu), torch.from_numpy(ki).to(gpu), torch.from_numpy(vi).to(gpu), out,
+                    1.0, 1.0, vs, False, -1)
+    assert rc == 0
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = np.broadcast_to(vi.astype(np.float64).mean(axis=2, keepdims=True) * vs, got.shape)
+    assert np.isfinite(got).all()
+    mx, _, _ = errors(got, want)
+    assert mx <= I8_MAX_ABS, f"max_abs {mx:.3e}"
+    assert np.all(np.abs(got[..., : d // 4] - 1.0) <= 1e-3) and np.all(np.abs(got[..., d // 4: d // 2] + 1.0) <= 1e-3)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_int8_saturated_scores(gpu, d, causal):
+    """q_scale = k_scale = 1 with every Q and K entry 127: each score is
+    127^2 D and s = 127^2 D / sqrt(D) log2(e) is of order 10^5, where fp32
+    carries only a few fractional bits.  Every visible key has the same
+    score, so p = 1 and pq must be the reference's min(127, lround(127 p)) =
+    127 -- a quantised P of 128 would read as -128 in an int8 operand and
+    flip the sign of the output.  The output is the mean of the visible V
+    rows times v_scale (closed form; causal: a running mean)."""
+    log(f"[int8 saturated] d{d} causal={causal}")
+    b, h, s = 1, 2, 300
+    rng = np.random.default_rng(12)
+    qi = np.full((b, h, s, d), 127, np.int8)
+    ki = np.full((b, h, s, d), 127, np.int8)
+    vi = rng.integers(-127, 128, (b, h, s, d), dtype=np.int8)
+    vs = 1.0 / 127.0
+    out = torch.full((b, h, s, d), float("nan"), dtype=torch.float16, device=gpu)
+    rc = forward_i8(torch.from_numpy(qi).to(gpu), torch.from_numpy(ki).to(gpu), torch.from_numpy(vi).to(gpu), out,
+                    1.0, 1.0, vs, causal, -1)
+    assert rc == 0
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    vf = vi.astype(np.float64) * vs
+    if causal:
+        want = np.cumsum(vf, axis=2) / np.arange(1, s + 1)[None, None, :, None]
+    else:
+        want = np.broadcast_to(vf.mean(axis=2, keepdims=True), got.shape)
+    assert np.isfinite(got).all()
+    mx, _, _ = errors(got, want)
+    assert mx <= I8_MAX_ABS, f"max_abs {mx:.3e}"

@@ -96,3 +96,32 @@ def test_noalloc_refuses_oversize_scratch(gpu):
     assert torch.isnan(out.float()).all()
     del q, k, v, out
     torch.cuda.empty_cache()
+
+
+def test_noalloc_makes_no_allocation(gpu):
+    """After rdna_scratch_trim, calls of the no-allocation entry point that
+    need both scratch buffers (RoPE-rotated K and split-K partials) leave the
+    library's scratch cache empty and make no allocator call, while the
+    allocating entry point on the same inputs does cache its buffers."""
+    import rdnattention
+
+    log("[noalloc] no cache entry and no allocator call after trim")
+    L = lib()
+    dev = torch.cuda.current_device()
+    q, k, v, cos, sin = _inputs(gpu, 97, 2, 16, 4, 2, 5000, 64, True, True)
+    out = torch.empty_like(q)
+    torch.cuda.synchronize()
+    rdnattention.trim_scratch()
+    before = rdnattention.scratch_stats(dev)
+    assert before["entries"] == 0 and before["cached_bytes"] == 0
+    for _ in range(3):
+        assert _call(L.rdna_attention_forward_noalloc, q, k, v, out, True, -1, cos, sin) == 0, L.rdna_get_error()
+    torch.cuda.synchronize()
+    after = rdnattention.scratch_stats(dev)
+    assert after == before, (before, after)
+    # the allocating entry point on the same call takes (and caches) two buffers
+    assert _call(L.rdna_attention_forward, q, k, v, out, True, -1, cos, sin) == 0, L.rdna_get_error()
+    torch.cuda.synchronize()
+    cached = rdnattention.scratch_stats(dev)
+    assert cached["entries"] == 2 and cached["allocations"] == before["allocations"] + 2, cached
+    rdnattention.trim_scratch()
