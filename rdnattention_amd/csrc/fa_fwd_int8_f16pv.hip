@@ -40,7 +40,13 @@
 // Kernel structure is the FP16 ping-pong design (fa_fwd_f16.hip): 8 waves in
 // two groups alternating MFMA and VALU phases, S^T = K Q^T so a lane owns one
 // query column, and P^T going from the S accumulator straight into the B
-// operand of O^T = V^T P^T.  V is converted to fp16 while it is staged into
+// operand of O^T = V^T P^T.  An MFMA phase issues the Q K^T MFMAs first and
+// the P V MFMAs after them, with the dequantisation of the scores riding on
+// the P V MFMAs.  Per score the softmax side costs one dequantisation fma
+// (the Q K^T chains start at the bit pattern of 1.5 2^23, so the int32 sum
+// read as fp32 is 1.5 2^23 + S), half a max3, the exponent fma, the
+// exponent, the row-sum add, one v_fma_mix (fp16(1 + 127 p 2^-10) rounds
+// 127 p to an integer) and half a packed fma (times the reference factor).  V is converted to fp16 while it is staged into
 // LDS (a byte permute against the fp16 exponent of 1024, then one packed
 // subtract; with a per-token V scale, fp16(sat(v * vs)) per row) and its V^T
 // operands come from ds_read_b64_tr_b16 transpose reads.  The grid is
@@ -92,8 +98,14 @@ struct I8Cfg {
     static constexpr int LDO = D + 8; // halves; output staging rows (conflict-free like K rows)
 };
 
-constexpr int kI8OpDepth = 4;                // MFMA operands in flight in the MFMA phase
+constexpr int kI8OpDepth = 6;                // MFMA operands in flight in the MFMA phase (4: +1 %)
 constexpr float kI8RefThreshold = 8.0f;      // log2 units: P is scaled by at most 2^8 (127 * 256 < 65504)
+// Start of the Q K^T chains: the int32 bit pattern of this float (1.5 2^23),
+// so the accumulator read as fp32 is kI8Bias + S, exact for |S| < 2^22
+constexpr float kI8Bias = 12582912.0f;
+// P enters P V as pq f 2^-10 (the quantisation's fp16 step, see phase_v);
+// the output factor multiplies the 2^10 back
+constexpr float kI8PScale = 0x1p-10f;
 
 __device__ __forceinline__ i4 buffer_load_i4(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     typedef unsigned u4 __attribute__((ext_vector_type(4)));
@@ -160,7 +172,8 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
     using C = I8Cfg<D>;
     __shared__ __attribute__((aligned(16))) int8_t sKs[2 * C::TILE_K];
     __shared__ __attribute__((aligned(16))) _Float16 sVs[2 * C::TILE_V];
-    __shared__ __attribute__((aligned(16))) float sks[2][kI8BN];
+    __shared__ __attribute__((aligned(16))) float sks[2][kI8BN]; // K scale of each key of a tile
+    __shared__ __attribute__((aligned(16))) float sbk[2][kI8BN]; // -kI8Bias * that scale
     __shared__ __attribute__((aligned(16))) _Float16 sO[kI8Waves * 32 * C::LDO];
 
     const int tid = threadIdx.x;
@@ -230,6 +243,8 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
         }
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
+        // class of key tile t_begin + i for this wave's rows (0 skip, 1 no mask, 2 masked)
+        const TileClasses tcls = wave_active ? tile_classes<kI8BN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
         f16x oacc[C::NDT];
 #pragma unroll
@@ -239,6 +254,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
         // m_run: the scheme's exact running max; m_ref: the lagging reference
         // O and l are kept relative to (m_ref <= m_run)
         float m_run = -INFINITY, m_ref = -INFINITY, l_run = 0.0f;
+        const i16x bias16 = SCORES ? i16x{} : (i16x{} + __float_as_int(kI8Bias));
         f16x tsc[2]; // scores of the current tile, dequantised by ks (t = S * ks)
         tsc[0] = f16x{};
         tsc[1] = f16x{};
@@ -308,36 +324,71 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
                 }
             }
             if (grp == 0 && gtid < kI8BN && x < n) {
-                sks[x & 1][gtid] = ksreg;
+                // ks rounded to 22 significant bits (relative change <= 2^-23),
+                // so that kI8Bias ks = 3 2^22 ks is exact in fp32 and the
+                // dequantisation fma returns S ks rounded once
+                const float ks22 = __uint_as_float((__float_as_uint(ksreg) + 2u) & ~3u);
+                sks[x & 1][gtid] = ks22;
+                sbk[x & 1][gtid] = -kI8Bias * ks22;
             }
         };
 
-        // M(i): O^T += V(i-1)^T P(i-1)^T (fp16 MFMA, i >= 1) then S(i)^T = K(i) Q^T
-        // (int8 MFMA, i < n): one stream of MFMAs whose LDS operands are read
-        // kI8OpDepth MFMAs ahead through a register ring
+        // M(i): S(i)^T = K(i) Q^T (int8 MFMA, i < n) then O^T += V(i-1)^T P(i-1)^T
+        // (fp16 MFMA, i >= 1): one stream of MFMAs whose LDS operands are read
+        // kI8OpDepth MFMAs ahead through a register ring.  The dequantisation
+        // of S(i) rides on the P V MFMAs: 8 groups of 4 scores, group u after
+        // P V MFMA 2u + 1, its K scales and biases read at MFMA 2u (at head
+        // dim 64, 8 P V MFMAs: group u after MFMA u).  (With the
+        // P V MFMAs first it ran after the last Q K^T MFMA, on the phase's
+        // critical path.)
         auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
             constexpr bool DO_PV = decltype(do_pv_c)::value;
             constexpr bool DO_S = decltype(do_s_c)::value;
+            constexpr bool DQ = DO_S && !SCORES;
+            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (st, kt)
             constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
-            constexpr int NSK = DO_S ? 2 * C::NS : 0;   // (s, kt)
-            constexpr int T = NPV + NSK;
+            static_assert(!DO_PV || NPV == 16 || NPV == 8, "8 dequantisation groups over the P V MFMAs");
+            constexpr int T = NSK + NPV;
             constexpr int DEPTH = T < kI8OpDepth ? T : kI8OpDepth;
             const int j16 = lane & 15;
             const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
                                    16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
             const int8_t* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 16 * g;
             auto op = [&](int j) -> i4 {
-                if (j < NPV) {
-                    const int u = j / C::NDT, dt = j % C::NDT;
-                    const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
-                    h4 lo = lds_read_tr16(base);
-                    h4 hi = lds_read_tr16(base + 8 * C::LDV);
-                    return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                if (j < NSK) {
+                    const int st = j >> 1, kt = j & 1;
+                    return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
                 }
-                const int js = j - NPV, st = js >> 1, kt = js & 1;
-                return *reinterpret_cast<const i4*>(krow + kt * 32 * C::LDK + 32 * st);
+                const int jp = j - NSK, u = jp / C::NDT, dt = jp % C::NDT;
+                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                h4 lo = lds_read_tr16(base);
+                h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                return __builtin_bit_cast(i4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             };
+            // SCORES: the raw int32 sums.  Otherwise each chain starts at the bit
+            // pattern of kI8Bias, so the int32 result is the fp32 number
+            // kI8Bias + S (exact: |S| <= 127^2 D < 2^22, the ulp there is 1)
+            const i16x start = SCORES ? i16x{} : bias16;
             i16x acc0 = {}, acc1 = {};
+            // dequantisation group u (keys 32 kt + 8 r4 + 4 g .. +3, kt = u / 4,
+            // r4 = u % 4), one fma per score: t = (kI8Bias + S) ks - kI8Bias ks,
+            // both terms exact (ks has 22 significant bits)
+            const float* ksl = sks[i & 1];
+            const float* bkl = sbk[i & 1];
+            f4 gks = {}, gbk = {};
+            auto dq_load = [&](int u) {
+                const int o = 32 * (u >> 2) + 8 * (u & 3) + 4 * g;
+                gks = *reinterpret_cast<const f4*>(&ksl[o]);
+                gbk = *reinterpret_cast<const f4*>(&bkl[o]);
+            };
+            auto dq_apply = [&](int u) {
+                const int kt = u >> 2, r4 = u & 3;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int32_t sv = kt == 0 ? acc0[4 * r4 + e] : acc1[4 * r4 + e];
+                    tsc[kt][4 * r4 + e] = fmaf(__int_as_float(sv), gks[e], gbk[e]);
+                }
+            };
             i4 ring[DEPTH > 0 ? DEPTH : 1];
 #pragma unroll
             for (int j = 0; j < DEPTH; j++) {
@@ -349,15 +400,25 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
                 if (j + DEPTH < T) {
                     ring[j % DEPTH] = op(j + DEPTH);
                 }
-                if (j < NPV) {
-                    const int u = j / C::NDT, dt = j % C::NDT;
-                    oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
-                } else {
-                    const int js = j - NPV, st = js >> 1;
-                    if (js & 1) {
-                        acc1 = mfma_32x32x32_i8(a, qreg[st], acc1);
+                if (j < NSK) {
+                    const int st = j >> 1;
+                    if (j & 1) {
+                        acc1 = mfma_32x32x32_i8(a, qreg[st], st == 0 ? start : acc1);
                     } else {
-                        acc0 = mfma_32x32x32_i8(a, qreg[st], acc0);
+                        acc0 = mfma_32x32x32_i8(a, qreg[st], st == 0 ? start : acc0);
+                    }
+                } else {
+                    const int jp = j - NSK, u = jp / C::NDT, dt = jp % C::NDT;
+                    oacc[dt] = mfma_32x32x16_f16(__builtin_bit_cast(h8, a), pb[u], oacc[dt]);
+                    if constexpr (DQ && NPV == 16) {
+                        if (jp & 1) {
+                            dq_apply(jp >> 1);
+                        } else {
+                            dq_load(jp >> 1);
+                        }
+                    } else if constexpr (DQ) {
+                        dq_load(jp);
+                        dq_apply(jp);
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -379,18 +440,11 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
                         }
                     }
                 }
-            } else if constexpr (DO_S) {
-                // dequantise here: the MFMA phase is the shorter one of the two
-                const float* ksl = sks[i & 1];
+            } else if constexpr (DQ && !DO_PV) {
 #pragma unroll
-                for (int r4 = 0; r4 < 4; r4++) {
-                    const f4 ks0 = *reinterpret_cast<const f4*>(&ksl[8 * r4 + 4 * g]);
-                    const f4 ks1 = *reinterpret_cast<const f4*>(&ksl[32 + 8 * r4 + 4 * g]);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        tsc[0][4 * r4 + e] = (float)acc0[4 * r4 + e] * ks0[e];
-                        tsc[1][4 * r4 + e] = (float)acc1[4 * r4 + e] * ks1[e];
-                    }
+                for (int u = 0; u < 8; u++) {
+                    dq_load(u);
+                    dq_apply(u);
                 }
             }
         };
@@ -399,11 +453,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
                 return;
             }
             const bool do_pv = !SCORES && i >= 1 && cls_prev != 0;
-            int cls_now = 0;
-            if (i < n) {
-                const int kt0 = (t_begin + i) * kI8BN;
-                cls_now = classify_tile(p.mask, q0, q_hi, kt0, kt0 + kI8BN - 1);
-            }
+            const int cls_now = i < n ? tile_class(tcls, t_begin + i) : 0;
             using T_ = std::true_type;
             using F_ = std::false_type;
             if (do_pv && cls_now != 0) {
@@ -423,7 +473,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
             if (SCORES || !wave_active || cls_prev == 0) {
                 return;
             }
-            f16x t[2] = {tsc[0], tsc[1]};
+            f16x (&t)[2] = tsc; // in place: a copy cost 16 moves per tile
             if (!qpos) {
 #pragma unroll
                 for (int kt = 0; kt < 2; kt++) {
@@ -472,20 +522,24 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
             // m_ref = -inf only while m_run = -inf (no visible key yet: every p is 0)
             const _Float16 f16 = (_Float16)(m_ref == -INFINITY ? 1.0f : fast_exp2(m_run - m_ref));
             const float c0 = int8_exp_offset(m_run);
+            const h2 fv = {f16, f16};
             float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const float y = fast_exp2(fmaf(t[kt][e], qeff, c0)); // 127 p, at most 127 (+ rounding)
-                    psum += y;
-                    pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)__builtin_rintf(y);
+                for (int e = 0; e < 16; e += 2) {
+                    // y = 127 p (<= 127); h = fp16(1 + y 2^-10) = 1 + round(y) 2^-10
+                    // (one v_fma_mix per score: [1, 2) has ulp 2^-10 in fp16),
+                    // then h f - f = pq f 2^-10, rounded once (one packed fma)
+                    const float y0 = fast_exp2(fmaf(t[kt][e], qeff, c0));
+                    const float y1 = fast_exp2(fmaf(t[kt][e + 1], qeff, c0));
+                    psum += y0;
+                    psum += y1;
+                    const h2 hq = {(_Float16)fmaf(y0, kI8PScale, 1.0f), (_Float16)fmaf(y1, kI8PScale, 1.0f)};
+                    const h2 pq = hq * fv - fv;
+                    pb[kt * 2 + (e >> 3)][e & 7] = pq[0];
+                    pb[kt * 2 + (e >> 3)][(e & 7) + 1] = pq[1];
                 }
-            }
-            const h8 fv = {f16, f16, f16, f16, f16, f16, f16, f16};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                pb[u] *= fv;
             }
             l_run = fmaf(psum, (float)f16, l_run);
         };
@@ -532,7 +586,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8_f16pv(Int8Params p)
         // O = O^T * v_scale / l (times the per-channel V scales of this kv head
         // when given), through this wave's sO slot
         const float l = pair_sum(l_run);
-        const float f = l > 0.0f ? p.v_scale / l : 0.0f;
+        const float f = l > 0.0f ? p.v_scale / (l * kI8PScale) : 0.0f;
         const float* vch = p.vch != nullptr ? p.vch + ((int64_t)b * p.Hkv + kvh) * D : nullptr;
         store_o_tile<D, C::LDO>(
             oacc,
