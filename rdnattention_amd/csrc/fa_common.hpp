@@ -86,6 +86,40 @@ __device__ __forceinline__ float sum_h8(h8 v, float acc) {
     return acc;
 }
 
+// Max of v(0) .. v(N - 1) as a tree of v_max3 (depth ceil(log3 N)) instead of
+// a chain: dependent VALU instructions issue about 8 cycles apart (a chain of
+// dependent fmas measured 7.8 cycles each), so the 16-deep v_max3 chain of a
+// 32-score row cost ~130 cycles of latency before any exponential could start.
+template <int N, class V>
+__device__ __forceinline__ float max_tree(V&& v) {
+    static_assert(N >= 1, "max of no values");
+    if constexpr (N == 1) {
+        return v(0);
+    } else if constexpr (N == 2) {
+        return fmaxf(v(0), v(1));
+    } else if constexpr (N == 3) {
+        return fmaxf(fmaxf(v(0), v(1)), v(2));
+    } else {
+        constexpr int M = (N + 2) / 3;
+        float m[M];
+#pragma unroll
+        for (int i = 0; i < M; i++) {
+            m[i] = 3 * i + 2 < N ? fmaxf(fmaxf(v(3 * i), v(3 * i + 1)), v(3 * i + 2))
+                                 : (3 * i + 1 < N ? fmaxf(v(3 * i), v(3 * i + 1)) : v(3 * i));
+        }
+        return max_tree<M>([&](int i) { return m[i]; });
+    }
+}
+
+// acc + the sum of the 32 halves of p[0..3], as four independent v_dot2c
+// chains of four (sum_h8 each) added in a fixed order, instead of one chain
+// of sixteen
+__device__ __forceinline__ float sum_h8x4(const h8 (&p)[4], float acc) {
+    const float s0 = sum_h8(p[0], 0.0f), s1 = sum_h8(p[1], 0.0f);
+    const float s2 = sum_h8(p[2], 0.0f), s3 = sum_h8(p[3], 0.0f);
+    return acc + ((s0 + s1) + (s2 + s3));
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt
 // [6:4], lgkmcnt [11:8]); the counters not named are left unwaited.
 constexpr int waitcnt_vm(int n) {

@@ -213,11 +213,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa_fwd_f16_decode(DecodeParams
                 sacc[e] = (off < a || off > bnd) ? -INFINITY : sacc[e];
             }
         }
-        float mx = sacc[0];
-#pragma unroll
-        for (int e = 1; e < 16; e++) {
-            mx = fmaxf(mx, sacc[e]);
-        }
+        float mx = max_tree<16>([&](int e) { return sacc[e]; });
         mx = pair_max(mx);
         const float m_new = fmaxf(m_run, mx * p.c);
         const bool grow = m_new > m_run + kDecRescaleThreshold;
@@ -234,14 +230,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void fa_fwd_f16_decode(DecodeParams
         }
         const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
         h8 pb[2];
-        float psum = 0.0f;
+        float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f}; // four independent chains
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const float pv = fast_exp2(fmaf(sacc[e], p.c, -m_use));
-            psum += pv;
+            ps[e & 3] += pv;
             pb[e >> 3][e & 7] = (_Float16)pv;
         }
-        l_run += psum;
+        l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
         // O^T += V^T P^T; V^T operand through transpose reads
         {

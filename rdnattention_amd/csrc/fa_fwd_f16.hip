@@ -396,15 +396,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                     }
                 }
             }
-            float mx = sacc[0][0];
-#pragma unroll
-            for (int e = 1; e < 16; e++) {
-                mx = fmaxf(mx, sacc[0][e]);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                mx = fmaxf(mx, sacc[1][e]);
-            }
+            float mx = max_tree<32>([&](int e) { return sacc[e >> 4][e & 15]; });
             mx = pair_max(mx);
             // PRE: sacc = S c - m_use already; otherwise S
             const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * p.c);
@@ -437,7 +429,6 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 }
                 m_use = m_use_new;
             }
-            float psum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; kt++) {
 #pragma unroll
@@ -446,11 +437,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                     pb[kt * 2 + (e >> 3)][e & 7] = (_Float16)fast_exp2(x);
                 }
             }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                psum = sum_h8(pb[u], psum);
-            }
-            l_run += psum;
+            l_run = sum_h8x4(pb, l_run);
         };
 
         // ---- prologue: pair 0 in LDS; each group's registers hold its next pair

@@ -351,11 +351,7 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
                     sacc[e] = (o8 < a || o8 > bnd) ? -INFINITY : sacc[e];
                 }
             }
-            float mx = sacc[0];
-#pragma unroll
-            for (int e = 1; e < 16; e++) {
-                mx = fmaxf(mx, sacc[e]);
-            }
+            float mx = max_tree<16>([&](int e) { return sacc[e]; });
             mx = pair_max(mx);
             // PRE: mx is a max of S c - m_use; otherwise of S (c > 0: -inf stays -inf)
             const float m_new = PRE ? fmaxf(m_run, mx + m_use) : fmaxf(m_run, mx * p.c);
@@ -387,7 +383,7 @@ __device__ __forceinline__ void dpair_half(const PrefillParams& p, char* smem, c
             for (int e = 0; e < 16; e++) {
                 pb[e >> 3][e & 7] = (_Float16)fast_exp2(PRE ? sacc[e] : fmaf(sacc[e], p.c, -m_use));
             }
-            l_run = sum_h8(pb[1], sum_h8(pb[0], l_run));
+            l_run += sum_h8(pb[0], 0.0f) + sum_h8(pb[1], 0.0f); // two independent chains
             xp[lane] = pb[0];
             xp[64 + lane] = pb[1];
             xa[lane] = alpha;
