@@ -16,39 +16,53 @@
 namespace rdna_amd {
 namespace {
 
-__global__ __launch_bounds__(256) void rope_rotate_rows(const _Float16* __restrict__ src, _Float16* __restrict__ dst,
-                                                        const float* __restrict__ cos_t,
-                                                        const float* __restrict__ sin_t, int64_t sb, int64_t sh,
-                                                        int64_t ss, int32_t H, int32_t S, int32_t D,
-                                                        int64_t n_chunks) {
-    const int chunks_per_row = D / 8;
+// Grid (row blocks, heads): block x is a run of kRopeRows rows, block y walks
+// the (b, h) pairs y, y + gridDim.y, ...; each thread rotates the 16-byte
+// chunks of one column (D / 8 threads per row), row after row, with no
+// division per chunk.  A flat index with three 64-bit divisions per chunk ran
+// at 5.8 TB/s.
+constexpr int kRopeThreads = 256;
+constexpr int kRopeRows = 64;
+
+__global__ __launch_bounds__(kRopeThreads) void rope_rotate_rows(const _Float16* __restrict__ src,
+                                                                 _Float16* __restrict__ dst,
+                                                                 const float* __restrict__ cos_t,
+                                                                 const float* __restrict__ sin_t, int64_t sb,
+                                                                 int64_t sh, int64_t ss, int32_t H, int32_t S,
+                                                                 int32_t D, int64_t heads) {
+    const int cpr = D / 8;                 // chunks per row
+    const int rpp = kRopeThreads / cpr;    // rows per pass (D <= 512: cpr <= 64)
+    const int ch = threadIdx.x % cpr;
+    const int r0 = threadIdx.x / cpr;
+    if (r0 >= rpp) {
+        return; // D / 8 does not divide the block (D = 96, 160, ...)
+    }
     const int half = D / 2;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n_chunks;
-         e += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t row = e / chunks_per_row;
-        const int ch = (int)(e - row * chunks_per_row);
-        const int64_t bh = row / S;
-        const int s = (int)(row - bh * S);
-        const int64_t b = bh / H;
-        const int h = (int)(bh - b * H);
-        h8 x = *reinterpret_cast<const h8*>(src + b * sb + h * sh + s * ss + 8 * ch);
-        x = rope8(x, cos_t + (int64_t)s * half, sin_t + (int64_t)s * half, 4 * ch);
-        *reinterpret_cast<h8*>(dst + row * D + 8 * ch) = x;
+    const int row_end = min(S, (int)(blockIdx.x + 1) * kRopeRows);
+    for (int64_t bh = blockIdx.y; bh < heads; bh += gridDim.y) {
+        const int64_t b = bh / H, h = bh - (bh / H) * H;
+        const _Float16* sp = src + b * sb + h * sh + 8 * ch;
+        _Float16* dp = dst + bh * S * D + 8 * ch;
+        for (int s = (int)blockIdx.x * kRopeRows + r0; s < row_end; s += rpp) {
+            h8 x = *reinterpret_cast<const h8*>(sp + (int64_t)s * ss);
+            x = rope8(x, cos_t + (int64_t)s * half, sin_t + (int64_t)s * half, 4 * ch);
+            __builtin_nontemporal_store(x, reinterpret_cast<h8*>(dp + (int64_t)s * D));
+        }
     }
 }
 
 } // namespace
 
 int rope_rotate_k(const AttnArgs& a, void* dst, hipStream_t stream, std::string& err) {
-    const int64_t n_chunks = (int64_t)a.B * a.Hkv * a.Sk * (a.D / 8);
-    if (n_chunks == 0) {
+    const int64_t heads = (int64_t)a.B * a.Hkv;
+    if (heads == 0 || a.Sk == 0) {
         return 0;
     }
-    const int64_t blocks64 = (n_chunks + 255) / 256;
-    const uint32_t blocks = (uint32_t)(blocks64 < 65536 ? blocks64 : 65536);
-    hipLaunchKernelGGL(rope_rotate_rows, dim3(blocks), dim3(256), 0, stream, static_cast<const _Float16*>(a.k),
-                       static_cast<_Float16*>(dst), a.rot_cos, a.rot_sin, a.ks[0], a.ks[1], a.ks[2], a.Hkv, a.Sk, a.D,
-                       n_chunks);
+    const uint32_t row_blocks = (uint32_t)((a.Sk + kRopeRows - 1) / kRopeRows);
+    const uint32_t head_blocks = (uint32_t)(heads < 65535 ? heads : 65535);
+    hipLaunchKernelGGL(rope_rotate_rows, dim3(row_blocks, head_blocks), dim3(kRopeThreads), 0, stream,
+                       static_cast<const _Float16*>(a.k), static_cast<_Float16*>(dst), a.rot_cos, a.rot_sin,
+                       a.ks[0], a.ks[1], a.ks[2], a.Hkv, a.Sk, a.D, heads);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         err = hipGetErrorString(e);

@@ -36,7 +36,10 @@ KernelTimerGuard::KernelTimerGuard(hipStream_t stream) : stream_(stream) {
     if (!g_timer_on.load(std::memory_order_relaxed)) {
         return;
     }
-    if (hipEventCreate(&start_) != hipSuccess || hipEventRecord(start_, stream_) != hipSuccess) {
+    // timing only: no system-scope fence (its L2 writeback would land inside
+    // the measured interval)
+    if (hipEventCreateWithFlags(&start_, hipEventDisableSystemFence) != hipSuccess ||
+        hipEventRecord(start_, stream_) != hipSuccess) {
         if (start_ != nullptr) {
             hipEventDestroy(start_);
         }
@@ -51,7 +54,8 @@ KernelTimerGuard::~KernelTimerGuard() {
         return;
     }
     hipEvent_t stop = nullptr;
-    if (hipEventCreate(&stop) != hipSuccess || hipEventRecord(stop, stream_) != hipSuccess) {
+    if (hipEventCreateWithFlags(&stop, hipEventDisableSystemFence) != hipSuccess ||
+        hipEventRecord(stop, stream_) != hipSuccess) {
         if (stop != nullptr) {
             hipEventDestroy(stop);
         }

@@ -166,7 +166,11 @@ int StreamScratch::alloc(size_t bytes, hipStream_t s, std::string& err) {
             }
             if (!per_call) {
                 if (ent.last_use == nullptr) {
-                    e = hipEventCreateWithFlags(&ent.last_use, hipEventDisableTiming);
+                    // device-scope only: the event orders GPU work (stream waits
+                    // and the trim's synchronisation before a stream-ordered
+                    // free); a system-scope release at each record would write
+                    // back the L2 after every attention kernel
+                    e = hipEventCreateWithFlags(&ent.last_use, hipEventDisableTiming | hipEventDisableSystemFence);
                 } else {
                     // after the buffer's previous use; a no-op when that use was
                     // on this same stream, and it orders a handle that now names
