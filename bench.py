@@ -556,6 +556,41 @@ def pmc_summary(directory: str) -> int:
     return 0
 
 
+def trace_steps(directory: str, main: str, last: int = 40) -> int:
+    """Per-step timeline of the last `last` steps from rocprofv3's
+    *kernel_trace.csv under `directory`.  A step ends with a dispatch whose
+    kernel name contains `main` and holds every dispatch since the previous
+    one: its time is end-to-end between the two main dispatches' ends, split
+    into each kernel's own time and the gaps between dispatches (launch and
+    completion latency, queue packets)."""
+    rows = []
+    for path in sorted(Path(directory).rglob("*kernel_trace.csv")):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                rows.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), row["Kernel_Name"]))
+    rows.sort()
+    ends = [i for i, r in enumerate(rows) if main in r[2]]
+    if len(ends) < 2:
+        print(f"fewer than two '{main}' dispatches under {directory}", file=sys.stderr)
+        return 1
+    ends = ends[-(last + 1):]
+    per_kernel, gaps, steps = {}, [], []
+    for a, b in zip(ends, ends[1:]):
+        step = rows[b][1] - rows[a][1]
+        busy = 0
+        for r in rows[a + 1:b + 1]:
+            name = r[2].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
+            per_kernel.setdefault(name, []).append(r[1] - r[0])
+            busy += r[1] - r[0]
+        steps.append(step)
+        gaps.append(step - busy)
+    n = len(steps)
+    print(f"steps={n} mean_step_us={sum(steps) / n / 1e3:.2f} gaps_us={sum(gaps) / n / 1e3:.2f}")
+    for name, d in per_kernel.items():
+        print(f"  {name:<62} per_step_us={sum(d) / n / 1e3:9.2f} calls_per_step={len(d) / n:.0f}")
+    return 0
+
+
 def pmc_derived(directory: str, mean):
     """Derived per-kernel figures from mean per-dispatch counters (and, when
     a run_kernel_trace.csv is present, mean dispatch durations):
@@ -632,11 +667,16 @@ def main(argv=None):
     ap.add_argument("--no-secondary", action="store_true", help="measure the selected workload only")
     ap.add_argument("--copy-calibration", action="store_true", help="run the 1 GiB copy used to scale counters")
     ap.add_argument("--pmc-summary", metavar="DIR", help="summarise rocprofv3 counter CSVs under DIR")
+    ap.add_argument("--trace-steps", nargs=2, metavar=("DIR", "KERNEL"),
+                    help="per-step kernel times and dispatch gaps of the last 40 steps ending with KERNEL, "
+                         "from rocprofv3 kernel-trace CSVs under DIR")
     ap.add_argument("--gemm-ceiling", type=int, metavar="N", default=0,
                     help="time an N^3 fp16 torch.matmul (the practical MFMA ceiling) and exit")
     args = ap.parse_args(argv)
     if args.pmc_summary:
         return pmc_summary(args.pmc_summary)
+    if args.trace_steps:
+        return trace_steps(args.trace_steps[0], args.trace_steps[1])
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(attention shards by (batch, kv head) with no exchange); run with --gpus 1", file=sys.stderr)

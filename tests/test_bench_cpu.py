@@ -130,3 +130,21 @@ def test_multi_gpu_refused():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_trace_steps_splits_kernels_and_gaps(tmp_path, capsys):
+    """bench.py --trace-steps on a synthetic kernel trace: two steps of a
+    5 us pre-pass and a 100 us main kernel with 2 us and 3 us gaps."""
+    import bench
+
+    rows = ["Kernel_Name,Start_Timestamp,End_Timestamp"]
+    t = 0
+    for _ in range(3):
+        rows.append(f"rope_rotate_rows,{t},{t + 5000}")
+        rows.append(f'"void rdna_amd::(anonymous namespace)::fa_fwd_f16_pp<128, true>(p)",{t + 7000},{t + 107000}')
+        t += 110000
+    (tmp_path / "run_kernel_trace.csv").write_text("\n".join(rows) + "\n")
+    assert bench.trace_steps(str(tmp_path), "fa_fwd_f16_pp<128") == 0
+    out = capsys.readouterr().out
+    assert "steps=2 mean_step_us=110.00 gaps_us=5.00" in out
+    assert "fa_fwd_f16_pp<128, true>" in out and "per_step_us=   100.00" in out
