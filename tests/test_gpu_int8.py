@@ -351,3 +351,73 @@ def test_int8_saturated_scores(gpu, d, causal):
     assert np.isfinite(got).all()
     mx, _, _ = errors(got, want)
     assert mx <= I8_MAX_ABS, f"max_abs {mx:.3e}"
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("per_token", [False, True])
+def test_int8_quantised_p_against_oracle_integers(gpu, oracle_lib, d, per_token):
+    """How often the kernel's quantised P differs from the reference's
+    integer pq = min(127, lround(127 p)) (src/rdna/fa2_forward_int8qk.hip:335,
+    restated by oracle.attention_int8).
+
+    One 64-key block per row and a one-hot V (row j of V is e_j) make the
+    output row the quantised P itself: o_ij = pq_ij * v_scale / (127 l_i).
+    The key with the row's largest score has p = 1 and pq = 127 in both, so
+    pq_ij = 127 o_ij / max_j o_ij; the fp16 output keeps that ratio to
+    2^-10, under 0.13 of a unit at pq = 127.  The kernel computes 127 p as
+    2^(s - m + log2 127) and rounds half to even, the oracle as
+    lroundf(127 exp2f(s - m)) with s rounded three times in fp32, so they
+    may part only where 127 p lies within a few fp32 rounding errors of
+    k + 1/2: every difference must be one unit, at such a point (checked in
+    float64 from the exact int32 scores), and rare."""
+    b, hq, sq, sk = 2, 8, 2048, 64
+    log(f"[int8 pq] d{d} per_token={per_token} B{b} Hq{hq} Sq{sq} Sk{sk}")
+    rng = np.random.default_rng(31 + d + per_token)
+    qi = rng.integers(-127, 128, (b, hq, sq, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (b, hq, sk, d), dtype=np.int8)
+    vi = np.zeros((b, hq, sk, d), np.int8)
+    vi[:, :, np.arange(sk), np.arange(sk)] = 1
+    # scores in the log2 domain spread over about +-4 * 2.5: p covers (0, 1]
+    if per_token:
+        qs = rng.uniform(0.012, 0.028, (b, hq, sq)).astype(np.float32)
+        ks = rng.uniform(0.012, 0.028, (b, hq, sk)).astype(np.float32)
+    else:
+        qs, ks = 0.02, 0.02
+    vs = 127.0
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)  # noqa: E731
+    out = torch.full((b, hq, sq, d), float("nan"), dtype=torch.float16, device=gpu)
+    rc = forward_i8(t(qi), t(ki), t(vi), out, t(qs) if per_token else qs, t(ks) if per_token else ks, vs, False, -1)
+    assert rc == 0
+    torch.cuda.synchronize()
+    full = out.float().cpu().numpy()
+    assert np.isfinite(full).all()
+    assert np.all(full[..., sk:] == 0)  # V columns past the 64 keys are zero
+    got = full[..., :sk].astype(np.float64)
+    emu = oracle.attention_int8(qi, ki, vi, qs, ks, vs)[..., :sk].astype(np.float64)
+
+    def integers(o):
+        y = 127.0 * o / o.max(axis=-1, keepdims=True)
+        pq = np.rint(y)
+        assert np.abs(y - pq).max() < 0.2
+        return pq.astype(np.int64)
+
+    pk, po = integers(got), integers(emu)
+    diff = pk - po
+    n_diff = int(np.count_nonzero(diff))
+    # 127 p in float64 from the exact scores: distance of each differing
+    # value from the nearest k + 1/2
+    s = oracle.int8_scores(qi, ki).astype(np.float64)
+    qsv = np.asarray(qs, np.float64)[..., None] if per_token else qs
+    ksv = np.asarray(ks, np.float64)[:, :, None, :] if per_token else ks
+    s = s * qsv * ksv * (d ** -0.5) * np.log2(np.e)
+    y = 127.0 * np.exp2(s - s.max(axis=-1, keepdims=True))
+    half_dist = np.abs(y - np.floor(y) - 0.5)
+    worst = float(half_dist[diff != 0].max()) if n_diff else 0.0
+    log(f"[int8 pq] d{d} per_token={per_token}: {n_diff} of {diff.size} differ "
+        f"({n_diff / diff.size:.2e}); nonzero pq {int(np.count_nonzero(po))}; "
+        f"largest |127p - (k+1/2)| among them {worst:.2e}")
+    assert np.abs(diff).max() <= 1
+    # measured on MI355X: 2 (d64) and 12 (d128) of 2,097,152 differ, all
+    # within 9.2e-5 of a tie
+    assert worst <= 5e-4
+    assert n_diff <= 2e-5 * diff.size

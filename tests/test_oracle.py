@@ -355,6 +355,34 @@ def test_int8_single_block_matches_gate_flavour(oracle_lib):
     assert diff.max() < 2e-2 * np.abs(gate).max()
 
 
+def test_int8_quantised_p_is_lround_of_127p(oracle_lib):
+    """One 64-key block and a one-hot V (row j = e_j) make the output row the
+    quantised P: o_ij = pq_ij * v_scale / (127 l_i).  The row's best key has
+    pq = 127, so pq_ij = 127 o_ij / max_j o_ij must be round(127 p_ij) with
+    p = 2^(s - max s), s = S qs ks scale log2(e) evaluated in float64 from
+    the exact int32 scores -- except within fp32 rounding of a tie at
+    k + 1/2.  A floor for the rounding, a 128 scale or a P taken against
+    another maximum fails (src/rdna/fa2_forward_int8qk.hip:301, :335)."""
+    rng = np.random.default_rng(7)
+    b, h, sq, sk, d = 1, 2, 256, 64, 64
+    qi = rng.integers(-127, 128, (b, h, sq, d), dtype=np.int8)
+    ki = rng.integers(-127, 128, (b, h, sk, d), dtype=np.int8)
+    vi = np.zeros((b, h, sk, d), np.int8)
+    vi[:, :, np.arange(sk), np.arange(sk)] = 1
+    qs = rng.uniform(0.012, 0.028, (b, h, sq)).astype(np.float32)
+    ks = rng.uniform(0.012, 0.028, (b, h, sk)).astype(np.float32)
+    o = oracle_lib.attention_int8(qi, ki, vi, qs, ks, 127.0).astype(np.float64)
+    y = 127.0 * o / o.max(axis=-1, keepdims=True)
+    pq = np.rint(y)
+    assert np.abs(y - pq).max() < 1e-4
+    s = oracle_lib.int8_scores(qi, ki).astype(np.float64) * qs[..., None] * ks[:, :, None, :]
+    s *= d ** -0.5 * np.log2(np.e)
+    want = 127.0 * np.exp2(s - s.max(axis=-1, keepdims=True))
+    off = pq != np.rint(want)
+    assert np.count_nonzero(pq) > 0.3 * pq.size  # P spans the quantiser's range
+    assert np.all(np.abs(want[off] - np.floor(want[off]) - 0.5) < 1e-4)
+
+
 def test_int8_blockwise_close_to_fp_attention(oracle_lib):
     """The quantised scheme approximates fp attention to the reference gate's bar
     (rel_rms < 5e-2, tests/hip_forward_int8qk_gate.hip:248)."""
