@@ -20,15 +20,22 @@
 //         its row sum; S(i)^T for the own keys; the own tile row max -> LDS
 //   V(i): the pair's max = max(own, partner's), the same in both halves, so
 //         both make the same rescale decisions; P(i) of the own keys -> LDS
-//         together with its row sum; staging of the next K/V tiles
+//         together with its row sum
 //
 // The row sum l adds the two halves' sums in one fixed order, so both halves
 // hold the same bits.  Everything else follows fa_fwd_f16_pp: S^T = K Q^T so a
 // lane owns one query column, P^T straight from the S accumulator into the
 // B operand of O^T = V^T P^T, V^T through transpose reads, the lazy max
-// (threshold 2^8), Q pre-scaled into log2 units (PRE), staging through
-// registers with each group storing its 32 rows of every tile, per-row-tile
-// tile classes, and (up to D = 192) a persistent grid.
+// (threshold 2^8), Q pre-scaled into log2 units (PRE), per-row-tile tile
+// classes, and (up to D = 192) a persistent grid.
+//
+// K/V tiles move HBM -> LDS by DMA (buffer_load ... lds), two rows per
+// instruction, issued by group B in its softmax phase; the row-pair LDS layout
+// (KPCfg) keeps both operand reads free of bank conflicts.  The issuing wave
+// waits on each DMA instruction (~70 cycles with four waves issuing), whatever
+// its size, so the instruction count sets the cost: one row per DMA cost more
+// than the register staging it replaced, and so did DMAs issued between the
+// MFMAs of group A's MFMA phase, which they stretched.
 #include "fa_common.hpp"
 #include "fa_host.hpp"
 #include "fa_internal.hpp"
@@ -50,40 +57,58 @@ constexpr int kKPWalkBlock = 32;           // row tiles that share a key-tile wa
 template <int D>
 struct KPCfg {
     static_assert(D % 32 == 0 && D >= 160 && D <= 256, "head_dim");
-    // LDS rows (halves): 16-row ds_read_b128 of K at 16-byte steps mod 256 B,
-    // 4-row transpose reads of V at a stride = 32 (mod 128) halves
-    static constexpr int LDK = D + 8;
-    static constexpr int LDV = D + ((32 - D % 128) + 128) % 128;
-    static constexpr int TILE_K = kKPBN * LDK;
-    static constexpr int TILE_V = kKPBN * LDV;
+    // K/V tiles in LDS as 32 row pairs (rows 2j, 2j + 1), each pair one
+    // 1 KB DMA: row 2j's chunk c (16 bytes) at byte 16 c of the pair, row
+    // 2j + 1's chunk c at byte 512 + 16 ((c + 8) mod 32).  Pairs lie PSK
+    // (PSV) halves apart, 16 (64) bytes more than 1 KB, so that
+    //   * the 16-row ds_read_b128 of a K chunk (rows r0 .. r0 + 15, r0 even)
+    //     falls on 16 distinct 16-byte bank groups mod 256 B: pair j at
+    //     16 j, the odd row a further 16 * 8 = 128 B on;
+    //   * the 8-row transpose reads of V (64 bytes per row) fall twice on
+    //     each 64-byte quarter of the banks: pair j at 64 j, odd rows +128 B.
+    static constexpr int PSK = 520; // halves per K row pair
+    static constexpr int PSV = 544; // halves per V row pair
+    static constexpr int ODD = 256; // halves from a pair's start to its odd row
+    static constexpr int ROT = 64;  // halves of the odd row's chunk rotation (8 chunks)
+    static constexpr int TILE_K = (kKPBN / 2) * PSK;
+    static constexpr int TILE_V = (kKPBN / 2) * PSV;
+    static constexpr int LDK = D + 8; // Q staging rows (halves): the K operand's conflict-free b128 reads
     static constexpr int NS = D / 16;               // Q K^T reduction steps
     static constexpr int DA = 32 * ((D + 63) / 64); // O^T columns of half 0
     static constexpr int DB = D - DA;               // ... of half 1
     static constexpr int KCH = D / 8;               // 16-byte chunks per K/V row
-    // staging of a group's 32 rows of a K (or V) tile: RPI rows per pass, KCH
-    // threads per row (RPI * KCH <= 256 threads busy), CT passes
-    static constexpr int RPI = 256 / KCH;
-    static constexpr int CT = (32 + RPI - 1) / RPI;
+    // group-B wave w moves row pairs 8w .. 8w + 7 of each K and V tile
+    static constexpr int DMA_PAIRS = kKPBN / 2 / 4;
+    static constexpr int NDMA = 2 * DMA_PAIRS; // DMA instructions per group-B wave per tile
     // exchange areas: P^T operands [wave][2][64 lanes] of 16 bytes, tile
     // maxima and row sums [wave][64 lanes] of 4 bytes
     static constexpr int KV_BYTES = (2 * TILE_K + 2 * TILE_V) * 2;
     // output staging after the key-tile loop, in the K/V area: [pair][32 rows][LDO]
     static constexpr int LDO = D + 8;
     static_assert(4 * 32 * LDO <= 2 * TILE_K + 2 * TILE_V, "output staging must fit the K/V area");
-    static_assert(KCH <= 32, "one row per 32 lanes");
+    // Q staging before the loop: the row tile's 128 rows at the LDK stride, in
+    // K slot 1 and the V slots, so that K(0) can land in K slot 0 meanwhile
+    static constexpr int Q_STAGE = TILE_K;
+    static_assert(4 * 32 * LDK <= TILE_K + 2 * TILE_V, "Q staging must fit K slot 1 and the V slots");
+    static_assert(KCH <= 32, "a row fits its 512 bytes of the pair");
     static constexpr int XP_BYTES = kKPWaves * 2 * 64 * 16;
     static constexpr int XS_BYTES = kKPWaves * 64 * 4;
     static constexpr int SMEM_BYTES = KV_BYTES + XP_BYTES + 2 * XS_BYTES;
-    // MFMA operands in flight (a 4-deep ring does not fit 256 registers at
-    // D = 256), and a persistent grid up to D = 192: at D = 224 and 256 it
-    // fits the registers but measured slower, since the static assignment
-    // loses the dispatch order that keeps concurrent row tiles on shared key
-    // tiles
-    static constexpr int OP_DEPTH = D <= 224 ? 4 : 3;
+    // MFMA operands in flight, and a persistent grid up to D = 192: at D = 224
+    // and 256 it fits the registers but measured slower, since the static
+    // assignment loses the dispatch order that keeps concurrent row tiles on
+    // shared key tiles
+    static constexpr int OP_DEPTH = 4;
     static constexpr bool PERSIST = D <= 192;
     static_assert(DB % 32 == 0 && DB > 0 && DA >= DB, "halves");
-    static_assert(LDV % 128 == 32 && LDV >= D, "V stride");
     static_assert(SMEM_BYTES <= 160 * 1024, "LDS");
+};
+
+// A group-B wave's DMA operands for one K/V tile pair: the two buffer
+// descriptors and the LDS addresses of the wave's first K and V row pairs.
+struct DmaPair {
+    i32x4_t rk, rv;
+    uint32_t mk, mv;
 };
 
 // The work of one half (C0, W) of every pair, over the persistent grid's
@@ -106,22 +131,21 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
     const int pair = wave >> 1;
     const int partner = wave ^ 1;
     const int grp = wave >> 2;  // 0 = group A, 1 = group B
-    const int gtid = tid & 255; // thread index inside the group
 
-    // ---- staging: this group's half (rows 32*grp .. +31) of K(x) and V(x-1).
-    // Thread gtid moves chunk ch of rows r0 + RPI*it: one base offset per
-    // thread, the pass's row step as the buffer load's scalar offset and as
-    // the LDS store's immediate offset.
-    const int srow = gtid / C::KCH; // < RPI for the busy threads
-    const int sch = gtid - srow * C::KCH;
-    const bool stager = srow < C::RPI;
-    const int r0 = 32 * grp + (stager ? srow : 0);
-    const uint32_t coff_k = (uint32_t)(((int64_t)r0 * p.k_ss + 8 * sch) * 2);
-    const uint32_t coff_v = (uint32_t)(((int64_t)r0 * p.v_ss + 8 * sch) * 2);
-    const int clk = r0 * C::LDK + 8 * sch;
-    const int clv = r0 * C::LDV + 8 * sch;
-    // pass it moves row r0 + RPI*it, inside the group's 32 rows
-    auto stages = [&](int it) { return stager && (32 % C::RPI == 0 || srow + C::RPI * it < 32); };
+    // ---- staging: K/V tiles move HBM -> LDS by DMA (buffer_load ... lds), one
+    // instruction per row pair: lane i moves global chunk c of row 2j + i / 32
+    // to LDS byte 16 i of the pair, c = i for i < 32 and c = (i - 32 + 24) mod
+    // 32 above (the odd row's rotation); lanes whose chunk lies past the row
+    // idle.  Only group B issues them, in its softmax phase: wave w of the
+    // group moves pairs 8w .. 8w + 7 of each K and V tile.  The pair's row
+    // offset is the instruction's scalar offset, its LDS address M0.
+    const uint32_t dma_j0 = (uint32_t)__builtin_amdgcn_readfirstlane((wave & 3) * C::DMA_PAIRS);
+    const int dma_c = lane < 32 ? lane : ((lane + 24) & 31);
+    const bool dma_lane = dma_c < C::KCH;
+    const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
+    const uint32_t dma_vk = (uint32_t)(lane >> 5) * k_row_b + 16u * (uint32_t)dma_c;
+    const uint32_t dma_vv = (uint32_t)(lane >> 5) * v_row_b + 16u * (uint32_t)dma_c;
+    const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
 
     auto run_tile = [&](const int wg) {
         int hg, rt;
@@ -175,61 +199,77 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             return t_begin + (u >= n ? u - n : u);
         };
         const int Sk = p.mask.sk;
-        const uint32_t k_row_b = (uint32_t)(p.k_ss * 2), v_row_b = (uint32_t)(p.v_ss * 2);
         int row_lo, row_hi;
         row_key_bounds(p.mask, q, row_lo, row_hi);
         // class of key tile T(i) for this pair's rows (0 skip, 1 no mask,
         // 2 masked): both halves of a pair share rows, so they share classes
         const TileClasses tcls = wave_active ? tile_classes<kKPBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
-        h8 kreg[C::CT], vreg[C::CT];
-        // Each group calls load_pair with x = 0, 1, 2, ... in order, so the
-        // tile addresses advance by one stride per call and step back n strides
-        // where the walk wraps (unsigned arithmetic: tiles past the walk, and V
-        // tile -1 of the first call, are never read; their num_records is 0).
+        // Group B sets up pair x = 0, 1, 2, ... in order: K(x) and V(x - 1).
+        // The tile addresses advance by one stride per pair and step back n
+        // strides where the walk wraps (unsigned arithmetic: tiles past the
+        // walk, and V tile -1 of pair 0, are never read; their num_records is
+        // 0, so their DMAs write zeros, into slots that no phase reads then).
         const uint64_t k_step = (uint64_t)(kKPBN * p.k_ss * 2), v_step = (uint64_t)(kKPBN * p.v_ss * 2);
         uint64_t k_addr = reinterpret_cast<uint64_t>(kbase) + (uint64_t)((int64_t)(t_begin + off) * kKPBN * p.k_ss * 2);
         uint64_t v_addr = reinterpret_cast<uint64_t>(vbase) + (uint64_t)((int64_t)(t_begin + off - 1) * kKPBN * p.v_ss * 2);
-        auto load_pair = [&](int x) {
+        auto uniform = [](i32x4_t r) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                r[e] = __builtin_amdgcn_readfirstlane(r[e]);
+            }
+            return r;
+        };
+        auto dma_pair = [&](int x) {
             const bool k_ok = x < n, v_ok = x >= 1 && x <= n;
             const int tk = k_ok ? walk(x) : 0, tv = v_ok ? walk(x - 1) : 0;
-            const auto rk = make_rsrc_uniform(k_addr, k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
-            const auto rv = make_rsrc_uniform(v_addr, v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
+            DmaPair d;
+            d.rk = uniform(make_rsrc_v(reinterpret_cast<const void*>(k_addr),
+                                       k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u));
+            d.rv = uniform(make_rsrc_v(reinterpret_cast<const void*>(v_addr),
+                                       v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u));
+            d.mk = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(lds0 + (uint32_t)(((x & 1) * C::TILE_K + (int)dma_j0 * C::PSK) * 2)));
+            d.mv = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(lds0 + (uint32_t)((2 * C::TILE_K + ((x - 1) & 1) * C::TILE_V + (int)dma_j0 * C::PSV) * 2)));
             // K(x + 1) is tile t_begin after the wrap at x + 1 + off = n;
             // V(x) likewise after the wrap at x + off = n
             k_addr += k_step - (x + 1 + off == n ? (uint64_t)n * k_step : 0);
             v_addr += v_step - (x + off == n ? (uint64_t)n * v_step : 0);
-#pragma unroll
-            for (int it = 0; it < C::CT; it++) {
-                if (stages(it)) {
-                    kreg[it] = buffer_load_h8(rk, coff_k, (uint32_t)(C::RPI * it) * k_row_b);
-                    vreg[it] = buffer_load_h8(rv, coff_v, (uint32_t)(C::RPI * it) * v_row_b);
+            return d;
+        };
+        // DMA k (0 <= k < NDMA) of a tile pair: row pair dma_j0 + k / 2 of
+        // the K tile (even k) or of the V tile (odd k)
+        auto dma_issue = [&](const DmaPair& d, int k) {
+            const uint32_t j = dma_j0 + (uint32_t)(k >> 1);
+            const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(2u * j * ((k & 1) ? v_row_b : k_row_b)));
+            if (dma_lane) {
+                if (k & 1) {
+                    dma_load16_s(d.rv, dma_vv, so, d.mv + (uint32_t)((k >> 1) * C::PSV * 2));
+                } else {
+                    dma_load16_s(d.rk, dma_vk, so, d.mk + (uint32_t)((k >> 1) * C::PSK * 2));
                 }
             }
         };
-        // LDS <- registers for pair x, whether or not the tiles exist: a
-        // missing tile was loaded as zeros into a slot that no phase reads,
-        // written on the same schedule as an existing tile (after the last
-        // read of the slot's previous contents)
-        auto store_pair = [&](int x) {
-            _Float16* sK = sKs + (x & 1) * C::TILE_K;
-            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
+        auto dma_all = [&](const DmaPair& d) {
 #pragma unroll
-            for (int it = 0; it < C::CT; it++) {
-                if (stages(it)) {
-                    *reinterpret_cast<h8*>(&sK[clk + C::RPI * it * C::LDK]) = kreg[it];
-                    *reinterpret_cast<h8*>(&sV[clv + C::RPI * it * C::LDV]) = vreg[it];
-                }
+            for (int k = 0; k < C::NDMA; k++) {
+                dma_issue(d, k);
             }
         };
 
-        // the first K/V pair is in flight while Q^T loads (full head dim,
-        // rotated and pre-scaled on the way)
-        if (n > 0) {
-            load_pair(0);
+        // K(0) is in flight while Q^T loads (full head dim, rotated and
+        // pre-scaled on the way); V(-1) is not issued, its slot holds Q
+        const bool dma_wave = __builtin_amdgcn_readfirstlane(grp) == 1;
+        if (dma_wave && n > 0) {
+            const DmaPair d0 = dma_pair(0);
+#pragma unroll
+            for (int k = 0; k < C::NDMA; k += 2) {
+                dma_issue(d0, k);
+            }
         }
-        // Q^T is staged through the K slots, which are free until the first
-        // K/V tile is stored.  Loaded in the operand layout, each lane would
+        // Q^T is staged through K slot 1 and the V slots, which are free until
+        // the first MFMA phase.  Loaded in the operand layout, each lane would
         // read 16 B of its own row, every load instruction touching 32 rows,
         // and the table loads came in chunks to bound the registers they
         // hold: one round trip per chunk.  Here all 512 threads load the row
@@ -237,10 +277,12 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         // with all loads of a thread in flight together, rotate and scale
         // them, and write them at the K rows' stride; each wave then reads
         // its pair's 32 rows with the K operand's conflict-free b128 reads.
+        // (These loads are issued after K(0)'s DMAs, so the compiler's waits
+        // for them also wait for the DMAs: never too early.)
         h8 qreg[C::NS];
         {
             constexpr int QCT = 4 * 32 * C::KCH / kKPThreads; // chunks per thread
-            static_assert(QCT * kKPThreads == 4 * 32 * C::KCH && 4 * 32 <= 2 * kKPBN, "Q chunks, Q in the K slots");
+            static_assert(QCT * kKPThreads == 4 * 32 * C::KCH, "Q chunks");
             const int hq0 = kvh * p.ratio + sub * p.G;
             const int gsh = p.G >> 1; // log2 G, G in {1, 2, 4}
             // chunk c of this thread: slot row rj (pair rj / 32), column chunk
@@ -291,16 +333,16 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
 #pragma unroll
             for (int c = 0; c < QCT; c++) {
                 const Chunk k = chunk(t, c);
-                *reinterpret_cast<h8*>(&sKs[k.rj * C::LDK + 8 * k.ch]) =
+                *reinterpret_cast<h8*>(&sKs[C::Q_STAGE + k.rj * C::LDK + 8 * k.ch]) =
                     k.qr < p.Sq ? (neg ? -x[c] : x[c]) : h8{};
             }
             __syncthreads();
-            const _Float16* src = sKs + (pair * 32 + l32) * C::LDK + 8 * g;
+            const _Float16* src = sKs + C::Q_STAGE + (pair * 32 + l32) * C::LDK + 8 * g;
 #pragma unroll
             for (int st = 0; st < C::NS; st++) {
                 qreg[st] = *reinterpret_cast<const h8*>(src + 16 * st);
             }
-            __syncthreads(); // every wave holds its Q^T before the K slots are overwritten
+            __syncthreads(); // every wave holds its Q^T before the Q area is overwritten
         }
 
         f16x oacc[NDT];
@@ -332,10 +374,21 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             constexpr int NSK = DO_S ? C::NS : 0;
             constexpr int T = NPV + NSK;
             constexpr int DEPTH = T < C::OP_DEPTH ? T : C::OP_DEPTH;
+            // Operand addresses in the row-pair layout: an odd row's chunk c
+            // sits ODD + ROT halves past where the even row's would, or ODD +
+            // ROT - 256 for c >= 24 (the rotation wraps).  K: row 32 HALF + l32,
+            // chunk 2 st + g, which wraps from st = 12.  V: rows 4 g + j16 / 4
+            // (+8, +16 u), columns C0 + 32 dt + 16 x + 4 (j16 % 4), which wrap
+            // where C0 + 32 dt >= 192.
             const int j16 = lane & 15;
-            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV + C0 +
-                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
-            const _Float16* krow = sKs + (i & 1) * C::TILE_K + (32 * HALF + l32) * C::LDK + 8 * g;
+            const int kodd = (l32 & 1) * 256;
+            const int vodd = ((j16 >> 2) & 1) * 256;
+            const _Float16* krow = sKs + (i & 1) * C::TILE_K + (16 * HALF + (l32 >> 1)) * C::PSK + 8 * g +
+                                   (kodd + (kodd >> 2));
+            const _Float16* krow_w = krow - kodd;
+            const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (2 * g + (j16 >> 3)) * C::PSV + C0 +
+                                   16 * ((lane >> 4) & 1) + 4 * (j16 & 3) + (vodd + (vodd >> 2));
+            const _Float16* vrow_w = vrow - vodd;
             // the partner's P^T operands (its 16-key groups u = 2 (1 - HALF) + j)
             h8 pop[2];
             if constexpr (DO_PV) {
@@ -344,12 +397,12 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             }
             auto op = [&](int j) -> h8 {
                 if (j < NSK) {
-                    return *reinterpret_cast<const h8*>(krow + 16 * j);
+                    return *reinterpret_cast<const h8*>((j < 12 ? krow : krow_w) + 16 * j);
                 }
                 const int jv = j - NSK, u = jv / NDT, dt = jv % NDT;
-                const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
+                const _Float16* base = (C0 + 32 * dt < 192 ? vrow : vrow_w) + (8 * u) * C::PSV + 32 * dt;
                 h4 lo = lds_read_tr16(base);
-                h4 hi = lds_read_tr16(base + 8 * C::LDV);
+                h4 hi = lds_read_tr16(base + 4 * C::PSV);
                 return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
             };
             f16x acc = {};
@@ -472,20 +525,22 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             xsum[wave * 64 + lane] = ps_own;
         };
 
-        if (n > 0) {
-            store_pair(0);
-            load_pair(1);
+        // K(0) landed (the DMAs are not tracked by the compiler's waits)
+        if (dma_wave) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         }
         __syncthreads();
-        // Both groups pass 2n + 2 barriers after the prologue's; group B
-        // starts one phase late.
+        // Group A: M(i) in phase 2i, V(i) in phase 2i + 1; group B one phase
+        // later.  K(i) is read in phases 2i and 2i + 1, V(i) in 2i + 2 and
+        // 2i + 3.  Group B issues K(i + 2) (K(i)'s slot) and V(i + 1) (V(i -
+        // 1)'s) at the start of its V(i), in phase 2i + 2, and waits for them
+        // at the end of its M(i + 1), phase 2i + 3; K(1) and V(0) in phase 0.
+        // Both groups pass 2n + 2 barriers after the prologue's.
         if (n > 0) {
             if (grp == 0) {
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
-                    store_pair(i + 1);
-                    load_pair(i + 2);
                     phase_v(i);
                     __syncthreads();
                 }
@@ -493,14 +548,15 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 __syncthreads();
                 __syncthreads();
             } else {
-                store_pair(1);
-                load_pair(2);
+                dma_all(dma_pair(1));
                 __syncthreads();
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
                     __syncthreads();
-                    store_pair(i + 2);
-                    load_pair(i + 3);
+                    if (i + 2 <= n) {
+                        dma_all(dma_pair(i + 2));
+                    }
                     phase_v(i);
                     __syncthreads();
                 }
