@@ -77,9 +77,16 @@ struct KPCfg {
     static constexpr int DA = 32 * ((D + 63) / 64); // O^T columns of half 0
     static constexpr int DB = D - DA;               // ... of half 1
     static constexpr int KCH = D / 8;               // 16-byte chunks per K/V row
-    // group-B wave w moves row pairs 8w .. 8w + 7 of each K and V tile
+    // Staging: by DMA from D = 224 (group-B wave w moves row pairs 8w .. 8w +
+    // 7 of each K and V tile), below through registers (each group its 32
+    // rows, RPI rows per pass, CT passes), which measured faster there: a DMA
+    // instruction costs the same however few of its lanes a short row fills
+    static constexpr bool DMA = D >= 224;
     static constexpr int DMA_PAIRS = kKPBN / 2 / 4;
     static constexpr int NDMA = 2 * DMA_PAIRS; // DMA instructions per group-B wave per tile
+    static constexpr int RPI = (256 / KCH) & ~1;
+    static constexpr int CT = (32 + RPI - 1) / RPI;
+    static_assert(DMA || RPI * KCH <= 256, "register staging: one chunk per thread and pass");
     // exchange areas: P^T operands [wave][2][64 lanes] of 16 bytes, tile
     // maxima and row sums [wave][64 lanes] of 4 bytes
     static constexpr int KV_BYTES = (2 * TILE_K + 2 * TILE_V) * 2;
@@ -146,6 +153,23 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
     const uint32_t dma_vk = (uint32_t)(lane >> 5) * k_row_b + 16u * (uint32_t)dma_c;
     const uint32_t dma_vv = (uint32_t)(lane >> 5) * v_row_b + 16u * (uint32_t)dma_c;
     const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    // Register staging (D <= 192): this group's rows 32 grp .. +31 of K(x)
+    // and V(x - 1); thread gtid moves chunk sch of rows r0 + RPI it (RPI even,
+    // so every row it moves has r0's parity): one base offset per thread, the
+    // pass's row step as the buffer load's scalar offset and as the LDS
+    // store's immediate offset.
+    const int gtid = tid & 255;
+    const int srow = gtid / C::KCH; // < RPI for the busy threads
+    const int sch = gtid - srow * C::KCH;
+    const bool stager = srow < C::RPI;
+    const int r0 = 32 * grp + (stager ? srow : 0);
+    const uint32_t coff_k = (uint32_t)(((int64_t)r0 * p.k_ss + 8 * sch) * 2);
+    const uint32_t coff_v = (uint32_t)(((int64_t)r0 * p.v_ss + 8 * sch) * 2);
+    const int cpos = (r0 & 1) * C::ODD + 8 * ((r0 & 1) ? ((sch + 8) & 31) : sch);
+    const int clk = (r0 >> 1) * C::PSK + cpos;
+    const int clv = (r0 >> 1) * C::PSV + cpos;
+    // pass it moves row r0 + RPI*it, inside the group's 32 rows
+    auto stages = [&](int it) { return stager && (32 % C::RPI == 0 || srow + C::RPI * it < 32); };
 
     auto run_tile = [&](const int wg) {
         int hg, rt;
@@ -258,15 +282,53 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             }
         };
 
-        // K(0) is in flight while Q^T loads (full head dim, rotated and
-        // pre-scaled on the way); V(-1) is not issued, its slot holds Q
-        const bool dma_wave = __builtin_amdgcn_readfirstlane(grp) == 1;
-        if (dma_wave && n > 0) {
-            const DmaPair d0 = dma_pair(0);
+        // Register staging: each group calls load_pair with x = 0, 1, 2, ...
+        // in order (the same address stepping) and stores pair x two phases
+        // later, whether or not the tiles exist: a missing tile was loaded as
+        // zeros into a slot that no phase reads, written on the same schedule
+        // as an existing tile (after the last read of the slot's previous
+        // contents).
+        h8 kreg[C::DMA ? 1 : C::CT], vreg[C::DMA ? 1 : C::CT];
+        auto load_pair = [&](int x) {
+            const bool k_ok = x < n, v_ok = x >= 1 && x <= n;
+            const int tk = k_ok ? walk(x) : 0, tv = v_ok ? walk(x - 1) : 0;
+            const auto rk = make_rsrc_uniform(k_addr, k_ok ? tile_bytes<kKPBN>(Sk - tk * kKPBN, k_row_b, D * 2) : 0u);
+            const auto rv = make_rsrc_uniform(v_addr, v_ok ? tile_bytes<kKPBN>(Sk - tv * kKPBN, v_row_b, D * 2) : 0u);
+            k_addr += k_step - (x + 1 + off == n ? (uint64_t)n * k_step : 0);
+            v_addr += v_step - (x + off == n ? (uint64_t)n * v_step : 0);
 #pragma unroll
-            for (int k = 0; k < C::NDMA; k += 2) {
-                dma_issue(d0, k);
+            for (int it = 0; it < C::CT; it++) {
+                if (stages(it)) {
+                    kreg[it] = buffer_load_h8(rk, coff_k, (uint32_t)(C::RPI * it) * k_row_b);
+                    vreg[it] = buffer_load_h8(rv, coff_v, (uint32_t)(C::RPI * it) * v_row_b);
+                }
             }
+        };
+        auto store_pair = [&](int x) {
+            _Float16* sK = sKs + (x & 1) * C::TILE_K;
+            _Float16* sV = sVs + ((x - 1) & 1) * C::TILE_V;
+#pragma unroll
+            for (int it = 0; it < C::CT; it++) {
+                if (stages(it)) {
+                    *reinterpret_cast<h8*>(&sK[clk + (C::RPI / 2) * it * C::PSK]) = kreg[it];
+                    *reinterpret_cast<h8*>(&sV[clv + (C::RPI / 2) * it * C::PSV]) = vreg[it];
+                }
+            }
+        };
+
+        // K(0) is in flight while Q^T loads (full head dim, rotated and
+        // pre-scaled on the way); V(-1) is not loaded by DMA, its slot holds Q
+        const bool dma_wave = __builtin_amdgcn_readfirstlane(grp) == 1;
+        if constexpr (C::DMA) {
+            if (dma_wave && n > 0) {
+                const DmaPair d0 = dma_pair(0);
+#pragma unroll
+                for (int k = 0; k < C::NDMA; k += 2) {
+                    dma_issue(d0, k);
+                }
+            }
+        } else if (n > 0) {
+            load_pair(0);
         }
         // Q^T is staged through K slot 1 and the V slots, which are free until
         // the first MFMA phase.  Loaded in the operand layout, each lane would
@@ -525,22 +587,33 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
             xsum[wave * 64 + lane] = ps_own;
         };
 
-        // K(0) landed (the DMAs are not tracked by the compiler's waits)
-        if (dma_wave) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        if constexpr (C::DMA) {
+            // K(0) landed (the DMAs are not tracked by the compiler's waits)
+            if (dma_wave) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            }
+        } else if (n > 0) {
+            store_pair(0);
+            load_pair(1);
         }
         __syncthreads();
         // Group A: M(i) in phase 2i, V(i) in phase 2i + 1; group B one phase
         // later.  K(i) is read in phases 2i and 2i + 1, V(i) in 2i + 2 and
-        // 2i + 3.  Group B issues K(i + 2) (K(i)'s slot) and V(i + 1) (V(i -
-        // 1)'s) at the start of its V(i), in phase 2i + 2, and waits for them
-        // at the end of its M(i + 1), phase 2i + 3; K(1) and V(0) in phase 0.
-        // Both groups pass 2n + 2 barriers after the prologue's.
+        // 2i + 3.  DMA: group B issues K(i + 2) (K(i)'s slot) and V(i + 1)
+        // (V(i - 1)'s) at the start of its V(i), in phase 2i + 2, and waits for
+        // them at the end of its M(i + 1), phase 2i + 3; K(1) and V(0) in phase
+        // 0.  Registers: each group stores pair i + 1 (A) or i + 2 (B) and
+        // loads the next in its V(i).  Both groups pass 2n + 2 barriers after
+        // the prologue's.
         if (n > 0) {
             if (grp == 0) {
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
+                    if constexpr (!C::DMA) {
+                        store_pair(i + 1);
+                        load_pair(i + 2);
+                    }
                     phase_v(i);
                     __syncthreads();
                 }
@@ -548,14 +621,26 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 __syncthreads();
                 __syncthreads();
             } else {
-                dma_all(dma_pair(1));
+                if constexpr (C::DMA) {
+                    dma_all(dma_pair(1));
+                } else {
+                    store_pair(1);
+                    load_pair(2);
+                }
                 __syncthreads();
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
-                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
+                    if constexpr (C::DMA) {
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
+                    }
                     __syncthreads();
-                    if (i + 2 <= n) {
-                        dma_all(dma_pair(i + 2));
+                    if constexpr (C::DMA) {
+                        if (i + 2 <= n) {
+                            dma_all(dma_pair(i + 2));
+                        }
+                    } else {
+                        store_pair(i + 2);
+                        load_pair(i + 3);
                     }
                     phase_v(i);
                     __syncthreads();
