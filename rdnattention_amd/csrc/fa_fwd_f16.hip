@@ -309,6 +309,13 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         // a small register ring; sched_barrier stops the compiler from hoisting
         // every read (which would need ~100 more VGPRs).
         auto mfma_stream = [&](auto do_pv_c, auto do_s_c, int i) {
+            // The MFMA phase runs at raised wave priority: each SIMD also holds
+            // the other group's wave in its softmax phase, whose VALU stream
+            // otherwise delays the issue of the next MFMA (-1.2 % on causal GQA
+            // B4 Hq32 Hkv8 S4096 D128 with RoPE and on B2 Hq32 Hkv8 S8192 D128 in
+            // same-box A/B runs; the INT8 head_dim 128 kernel, whose softmax
+            // side is its critical path, measured slower with it)
+            __builtin_amdgcn_s_setprio(1);
             constexpr bool DO_PV = decltype(do_pv_c)::value;
             constexpr bool DO_S = decltype(do_s_c)::value;
             constexpr int NPV = DO_PV ? 4 * C::NDT : 0; // (u, dt)
@@ -355,6 +362,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            __builtin_amdgcn_s_setprio(0);
             if constexpr (DO_S) {
                 sacc[0] = acc0;
                 sacc[1] = acc1;

@@ -335,6 +335,12 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
         // restarts its int32 chain; the dequantisation of S(i) rides on the P V
         // MFMAs.
         auto mfma_stream = [&](auto do_pv_c, auto do_s_c, auto fold_c, int i) {
+            // The MFMA phase runs at raised wave priority: each SIMD also holds
+            // the other group's wave in its softmax phase, whose VALU stream
+            // otherwise delays the issue of the next MFMA (-2.7 % at head_dim 64 in
+            // same-box A/B runs; the INT8 head_dim 128 kernel, whose softmax
+            // side is its critical path, measured slower with it)
+            __builtin_amdgcn_s_setprio(1);
             constexpr bool DO_PV = decltype(do_pv_c)::value;
             constexpr bool DO_S = decltype(do_s_c)::value;
             constexpr bool FOLD = decltype(fold_c)::value;
@@ -409,6 +415,7 @@ __global__ __launch_bounds__(kI8Threads, 1) void fa_fwd_int8(Int8Params p) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            __builtin_amdgcn_s_setprio(0);
             if constexpr (DO_S && SCORES) {
                 // the two S^T blocks of this tile: lane holds query q, keys
                 // kt0 + 32 kt + 8 (e / 4) + 4 g + e % 4
