@@ -55,6 +55,14 @@ constexpr float kRescaleThreshold = 8.0f; // log2 units
 // i % 2 and (i - 1) % 2.  Group A stages pair (K(i+1), V(i)) in its V(i)
 // (phase 2i+1), group B stages pair (K(i+2), V(i+1)) in its V(i) (phase 2i+2);
 // both write slots whose last readers finished before the preceding barrier.
+// At D = 128 group B alone moves both halves instead, by HBM -> LDS DMA (one
+// 1 KB instruction per 4-row group, eight per wave per tile) issued at the
+// start of its V(i) and awaited at the end of its M(i+1): the loads' issue and
+// the LDS stores left the softmax side, which is the longer one (0.4 % faster
+// on causal GQA B4 Hq32 Hkv8 S4096 D128 in same-box A/B runs, 16 fewer
+// registers, 7.7 KB less LDS).  Group A cannot issue with two phases of
+// latency: with two slots, K(i+2) and V(i+1) can be written only once group
+// B's M(i) has read K(i) and V(i-1).
 // ---------------------------------------------------------------------------
 constexpr int kPPWaves = 8;
 constexpr int kOpDepth = 4; // MFMA operands in flight in the MFMA phase
@@ -67,8 +75,18 @@ struct PPCfg {
     // are read 4 at a time, 64 B each, by the transpose read -> a 64 B step
     static constexpr int LDK = D + 8;
     static constexpr int LDV = D + 32;
-    static constexpr int TILE_K = kBN * LDK;
-    static constexpr int TILE_V = kBN * LDV;
+    // D = 128: K/V tiles staged by HBM -> LDS DMA, one instruction per 4-row
+    // group (1 KB).  Row 4j + b of a tile sits at byte 256 b of group j, its
+    // 16-byte chunk c at position c ^ 4b; groups lie PSK (PSV) halves apart,
+    // 16 (64) bytes more than 1 KB.  The 16-row b128 K reads then hit 16
+    // distinct 16-byte bank groups (group j at 16 j mod 256, row b's chunk
+    // moved by 64 b), and the 8-row transpose reads of V fall twice on each
+    // 64-byte quarter (group j at 64 j, row b's chunk quad moved by b).
+    static constexpr bool DMA = D == 128;
+    static constexpr int PSK = 520;
+    static constexpr int PSV = 544;
+    static constexpr int TILE_K = DMA ? (kBN / 4) * PSK : kBN * LDK;
+    static constexpr int TILE_V = DMA ? (kBN / 4) * PSV : kBN * LDV;
     static constexpr int NS = D / 16;
     static constexpr int NDT = D / 32;
     static constexpr int KCH = D / 8;
@@ -123,6 +141,16 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         clk[it] = ok ? row * C::LDK + 8 * ch : -1;
         clv[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
+    // DMA staging (PPCfg::DMA): group B's wave w moves 4-row groups 4w .. 4w + 3
+    // of each K and V tile, lane i global chunk (i % 16) ^ 4 (i / 16) of row
+    // 4j + i / 16 to LDS byte 16 i of group j; the group's row offset is the
+    // instruction's scalar offset, its LDS address M0.
+    const uint32_t dma_j0 = (uint32_t)__builtin_amdgcn_readfirstlane((wave & 3) * 4);
+    const uint32_t dma_c = (uint32_t)((lane & 15) ^ (4 * (lane >> 4)));
+    const uint32_t dma_vk = (uint32_t)(lane >> 4) * (uint32_t)(p.k_ss * 2) + 16u * dma_c;
+    const uint32_t dma_vv = (uint32_t)(lane >> 4) * (uint32_t)(p.v_ss * 2) + 16u * dma_c;
+    const uint32_t lds_k = (uint32_t)reinterpret_cast<uintptr_t>(sKs);
+    const uint32_t lds_v = (uint32_t)reinterpret_cast<uintptr_t>(sVs);
     // Persistent (PPCfg::PERSIST): this workgroup walks its share of the row
     // tiles (one per workgroup of a one-tile-per-workgroup grid, see
     // persistent_item). Every group passes the same barriers per item and
@@ -304,6 +332,45 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             }
         };
 
+        // DMA staging: group B sets up pair x = 0, 1, 2, ... in order (the same
+        // address stepping as load_pair) and issues its 8 DMAs: K group
+        // dma_j0 + k / 2 for even k, V group dma_j0 + k / 2 for odd k.
+        struct DmaPair {
+            i32x4_t rk, rv;
+            uint32_t mk, mv;
+        };
+        auto uniform = [](i32x4_t r) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                r[e] = __builtin_amdgcn_readfirstlane(r[e]);
+            }
+            return r;
+        };
+        auto dma_pair = [&](int x) {
+            const int tk = t_begin + x, tv = t_begin + x - 1;
+            DmaPair d;
+            d.rk = uniform(make_rsrc_v(reinterpret_cast<const void*>(k_addr),
+                                       x < n ? tile_bytes<kBN>(Sk - tk * kBN, k_row_b, D * 2) : 0u));
+            d.rv = uniform(make_rsrc_v(reinterpret_cast<const void*>(v_addr),
+                                       (x >= 1 && x <= n) ? tile_bytes<kBN>(Sk - tv * kBN, v_row_b, D * 2) : 0u));
+            d.mk = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(lds_k + (uint32_t)(((x & 1) * C::TILE_K + (int)dma_j0 * C::PSK) * 2)));
+            d.mv = (uint32_t)__builtin_amdgcn_readfirstlane(
+                (int)(lds_v + (uint32_t)((((x - 1) & 1) * C::TILE_V + (int)dma_j0 * C::PSV) * 2)));
+            k_addr += k_step;
+            v_addr += v_step;
+            return d;
+        };
+        auto dma_issue = [&](const DmaPair& d, int k) {
+            const uint32_t j = dma_j0 + (uint32_t)(k >> 1);
+            const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane((int)(4u * j * ((k & 1) ? v_row_b : k_row_b)));
+            if (k & 1) {
+                dma_load16_s(d.rv, dma_vv, so, d.mv + (uint32_t)((k >> 1) * C::PSV * 2));
+            } else {
+                dma_load16_s(d.rk, dma_vk, so, d.mk + (uint32_t)((k >> 1) * C::PSK * 2));
+            }
+        };
+
         // M(i): O += V(i-1)^T P(i-1) (i >= 1) then S(i) = K(i) Q^T (i < n), as one
         // stream of MFMAs whose LDS operands are read kOpDepth MFMAs ahead through
         // a small register ring; sched_barrier stops the compiler from hoisting
@@ -326,15 +393,46 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             const _Float16* vrow = sVs + ((i - 1) & 1) * C::TILE_V + (4 * g + (j16 >> 2)) * C::LDV +
                                    16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
             const _Float16* krow = sKs + (i & 1) * C::TILE_K + l32 * C::LDK + 8 * g;
+            // DMA layout: K row l32 (+32 kt) is row b = l32 % 4 of group l32 / 4
+            // (+8 kt), its chunk 2 st + g at position 2 (st ^ 2b) + g, i.e. at
+            // 16 (st % 2) + 32 ((st / 2) ^ b) halves: one base per st / 2.  V
+            // row 16u + 8h + 4g + j16 / 4 is row b = j16 / 4 of group 4u + 2h + g,
+            // its columns 32 dt + 16 x + 4 (j16 % 4) at chunk quad dt ^ b: one
+            // base per dt.
+            const _Float16* kb[C::DMA ? 4 : 1];
+            const _Float16* vb[C::DMA ? C::NDT : 1];
+            if constexpr (C::DMA) {
+                const int bk = l32 & 3, bv = (j16 >> 2) & 3;
+                const _Float16* k0 = sKs + (i & 1) * C::TILE_K + (l32 >> 2) * C::PSK + 128 * bk + 8 * g;
+                const _Float16* v0 = sVs + ((i - 1) & 1) * C::TILE_V + g * C::PSV + 128 * bv +
+                                     16 * ((lane >> 4) & 1) + 4 * (j16 & 3);
+#pragma unroll
+                for (int s2 = 0; s2 < 4; s2++) {
+                    kb[s2] = k0 + 32 * (s2 ^ bk);
+                }
+#pragma unroll
+                for (int dt = 0; dt < C::NDT; dt++) {
+                    vb[dt] = v0 + 32 * (dt ^ bv);
+                }
+            }
             auto op = [&](int j) -> h8 {
                 if (j < NPV) {
                     const int u = j / C::NDT, dt = j % C::NDT;
+                    if constexpr (C::DMA) {
+                        const _Float16* base = vb[dt] + (4 * u) * C::PSV;
+                        h4 lo = lds_read_tr16(base);
+                        h4 hi = lds_read_tr16(base + 2 * C::PSV);
+                        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                    }
                     const _Float16* base = vrow + (16 * u) * C::LDV + 32 * dt;
                     h4 lo = lds_read_tr16(base);
                     h4 hi = lds_read_tr16(base + 8 * C::LDV);
                     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
                 const int js = j - NPV, st = js >> 1, kt = js & 1;
+                if constexpr (C::DMA) {
+                    return *reinterpret_cast<const h8*>(kb[st >> 1] + kt * 8 * C::PSK + 16 * (st & 1));
+                }
                 return *reinterpret_cast<const h8*>(krow + kt * 32 * C::LDK + 16 * st);
             };
             f16x acc0 = {}, acc1 = {};
@@ -449,11 +547,25 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         };
 
         // ---- prologue: pair 0 in LDS; each group's registers hold its next pair
-        if (n > 0) {
+        // (DMA: group B's K(0) in flight while Q stages)
+        const bool dma_wave = __builtin_amdgcn_readfirstlane(grp) == 1;
+        if constexpr (C::DMA) {
+            if (dma_wave && n > 0) {
+                const DmaPair d0 = dma_pair(0);
+#pragma unroll
+                for (int k = 0; k < 8; k += 2) {
+                    dma_issue(d0, k);
+                }
+            }
+        } else if (n > 0) {
             load_pair(0);
         }
         stage_q();
-        if (n > 0) {
+        if constexpr (C::DMA) {
+            if (dma_wave) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(0) landed (not tracked by the compiler)
+            }
+        } else if (n > 0) {
             store_pair(0);
             load_pair(1);
         }
@@ -465,8 +577,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
-                    store_pair(i + 1);
-                    load_pair(i + 2);
+                    if constexpr (!C::DMA) {
+                        store_pair(i + 1);
+                        load_pair(i + 2);
+                    }
                     phase_v(i);
                     __syncthreads();
                 }
@@ -474,14 +588,38 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 __syncthreads();
                 __syncthreads();
             } else {
-                store_pair(1);
-                load_pair(2);
+                // DMA: group B issues K(i + 2) and V(i + 1) at the start of its V(i)
+                // and waits for them at the end of its M(i + 1); K(1) and V(0)
+                // in phase 0
+                if constexpr (C::DMA) {
+                    const DmaPair d1 = dma_pair(1);
+#pragma unroll
+                    for (int k = 0; k < 8; k++) {
+                        dma_issue(d1, k);
+                    }
+                } else {
+                    store_pair(1);
+                    load_pair(2);
+                }
                 __syncthreads();
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
+                    if constexpr (C::DMA) {
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
+                    }
                     __syncthreads();
-                    store_pair(i + 2);
-                    load_pair(i + 3);
+                    if constexpr (C::DMA) {
+                        if (i + 2 <= n) {
+                            const DmaPair d = dma_pair(i + 2);
+#pragma unroll
+                            for (int k = 0; k < 8; k++) {
+                                dma_issue(d, k);
+                            }
+                        }
+                    } else {
+                        store_pair(i + 2);
+                        load_pair(i + 3);
+                    }
                     phase_v(i);
                     __syncthreads();
                 }
