@@ -345,9 +345,12 @@ def test_wave_pair_split_gqa(gpu, oracle_lib, d, hq, hkv):
     assert_f16_parity(out.float().cpu().numpy(), ref, f"split d{d} gqa {hq}/{hkv}")
 
 
-@pytest.mark.parametrize("d", [288, 512])
+@pytest.mark.parametrize("d", [160, 224, 256, 288, 512])
 def test_large_head_strided_kv_bit_identical(gpu, oracle_lib, d):
-    """Large-head kernel with K/V sliced from one [B,S,2,Hkv,D] buffer."""
+    """Large-head kernels with K/V sliced from one [B,S,2,Hkv,D] buffer: the
+    wave-pair kernel's register staging (160) and two-row DMA staging (224,
+    256, where a DMA's second row is one sequence stride past the first) and
+    the head-dimension pair kernel (288, 512)."""
     g = torch.Generator().manual_seed(9)
     b, hq, hkv, sq, sk = 1, 4, 2, 70, 133
     buf = torch.randn(b, sk, 2, hkv, d, generator=g).half().to(gpu)
