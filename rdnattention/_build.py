@@ -43,7 +43,8 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # every -inf - -inf case is selected away), so the five extra VALU per tile
 # are dropped.  Infinities keep IEEE semantics.  The quantisers keep the
 # default: their amax must treat NaN inputs as torch does.
-NO_NAN_SOURCES = {"fa_fwd_f16.hip", "fa_fwd_f16_kpair.hip", "fa_fwd_int8.hip", "fa_fwd_int8_f16pv.hip"}
+NO_NAN_SOURCES = {"fa_fwd_f16.hip", "fa_fwd_f16_kpair.hip", "fa_fwd_f16_dpair.hip", "fa_fwd_int8.hip",
+                  "fa_fwd_int8_f16pv.hip"}
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function", f"-I{ROOT / 'include'}"]
 
 
