@@ -55,14 +55,16 @@ constexpr float kRescaleThreshold = 8.0f; // log2 units
 // i % 2 and (i - 1) % 2.  Group A stages pair (K(i+1), V(i)) in its V(i)
 // (phase 2i+1), group B stages pair (K(i+2), V(i+1)) in its V(i) (phase 2i+2);
 // both write slots whose last readers finished before the preceding barrier.
-// At D = 128 group B alone moves both halves instead, by HBM -> LDS DMA (one
-// 1 KB instruction per 4-row group, eight per wave per tile) issued at the
-// start of its V(i) and awaited at the end of its M(i+1): the loads' issue and
-// the LDS stores left the softmax side, which is the longer one (0.4 % faster
-// on causal GQA B4 Hq32 Hkv8 S4096 D128 in same-box A/B runs, 16 fewer
-// registers, 7.7 KB less LDS).  Group A cannot issue with two phases of
-// latency: with two slots, K(i+2) and V(i+1) can be written only once group
-// B's M(i) has read K(i) and V(i-1).
+// At D = 128 the tiles move by HBM -> LDS DMA instead (one 1 KB instruction
+// per 4-row group): the loads' issue and the LDS stores left the softmax side,
+// which is the longer one (0.4 % faster on causal GQA B4 Hq32 Hkv8 S4096 D128
+// in same-box A/B runs, 16 fewer registers, 7.7 KB less LDS).  Group B issues
+// K(i+2) at the start of its V(i) and awaits it at the end of its M(i+1), two
+// phases of latency.  Group A issues V(i) at the start of its own V(i) and
+// awaits it at the end of that phase: V(i-2)'s slot was last read in phase
+// 2i-1, and V(i) is first read in phase 2i+2.  Each group's softmax side then
+// carries four DMAs per wave per tile instead of zero and eight (-0.8 % on the
+// causal GQA shape above, -1.1 % on causal GQA B2 Hq32 Hkv8 S8192 D128).
 // ---------------------------------------------------------------------------
 constexpr int kPPWaves = 8;
 constexpr int kOpDepth = 4; // MFMA operands in flight in the MFMA phase
@@ -83,6 +85,9 @@ struct PPCfg {
     // moved by 64 b), and the 8-row transpose reads of V fall twice on each
     // 64-byte quarter (group j at 64 j, row b's chunk quad moved by b).
     static constexpr bool DMA = D == 128;
+    // K tiles by group B, V tiles by group A in its own softmax phase (else
+    // both by group B)
+    static constexpr bool DMA_SPLIT = true;
     static constexpr int PSK = 520;
     static constexpr int PSV = 544;
     static constexpr int TILE_K = DMA ? (kBN / 4) * PSK : kBN * LDK;
@@ -141,8 +146,8 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         clk[it] = ok ? row * C::LDK + 8 * ch : -1;
         clv[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
-    // DMA staging (PPCfg::DMA): group B's wave w moves 4-row groups 4w .. 4w + 3
-    // of each K and V tile, lane i global chunk (i % 16) ^ 4 (i / 16) of row
+    // DMA staging (PPCfg::DMA): wave w of group B (K) or A (V) moves 4-row
+    // groups 4w .. 4w + 3 of each tile, lane i global chunk (i % 16) ^ 4 (i / 16) of row
     // 4j + i / 16 to LDS byte 16 i of group j; the group's row offset is the
     // instruction's scalar offset, its LDS address M0.
     const uint32_t dma_j0 = (uint32_t)__builtin_amdgcn_readfirstlane((wave & 3) * 4);
@@ -332,9 +337,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
             }
         };
 
-        // DMA staging: group B sets up pair x = 0, 1, 2, ... in order (the same
-        // address stepping as load_pair) and issues its 8 DMAs: K group
-        // dma_j0 + k / 2 for even k, V group dma_j0 + k / 2 for odd k.
+        // DMA staging: each group sets up pair x = 0, 1, 2, ... in order (the
+        // same address stepping as load_pair) and issues its half of the 8
+        // DMAs: K group dma_j0 + k / 2 for even k (group B), V group dma_j0 +
+        // k / 2 for odd k (group A).
         struct DmaPair {
             i32x4_t rk, rv;
             uint32_t mk, mv;
@@ -574,28 +580,43 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         // Both groups pass 2n + 2 barriers; group B starts one phase late.
         if (n > 0) {
             if (grp == 0) {
+                if constexpr (C::DMA && C::DMA_SPLIT) {
+                    (void)dma_pair(0); // the address stepping starts at pair 0
+                }
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
                     if constexpr (!C::DMA) {
                         store_pair(i + 1);
                         load_pair(i + 2);
+                    } else if constexpr (C::DMA_SPLIT) {
+                        // V(i) into V(i - 2)'s slot, last read in phase 2i - 1;
+                        // first read in phase 2i + 2
+                        const DmaPair d = dma_pair(i + 1);
+#pragma unroll
+                        for (int k = 1; k < 8; k += 2) {
+                            dma_issue(d, k);
+                        }
                     }
                     phase_v(i);
+                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // V(i) landed
+                    }
                     __syncthreads();
                 }
                 phase_m(n);
                 __syncthreads();
                 __syncthreads();
             } else {
-                // DMA: group B issues K(i + 2) and V(i + 1) at the start of its V(i)
-                // and waits for them at the end of its M(i + 1); K(1) and V(0)
-                // in phase 0
+                // DMA: group B issues K(i + 2) at the start of its V(i) and
+                // waits for it at the end of its M(i + 1); K(1) in phase 0
                 if constexpr (C::DMA) {
-                    const DmaPair d1 = dma_pair(1);
+                    if (!C::DMA_SPLIT || 1 < n) {
+                        const DmaPair d1 = dma_pair(1);
 #pragma unroll
-                    for (int k = 0; k < 8; k++) {
-                        dma_issue(d1, k);
+                        for (int k = 0; k < 8; k += C::DMA_SPLIT ? 2 : 1) {
+                            dma_issue(d1, k);
+                        }
                     }
                 } else {
                     store_pair(1);
@@ -609,10 +630,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                     }
                     __syncthreads();
                     if constexpr (C::DMA) {
-                        if (i + 2 <= n) {
+                        if (i + 2 < n || (!C::DMA_SPLIT && i + 2 == n)) {
                             const DmaPair d = dma_pair(i + 2);
 #pragma unroll
-                            for (int k = 0; k < 8; k++) {
+                            for (int k = 0; k < 8; k += C::DMA_SPLIT ? 2 : 1) {
                                 dma_issue(d, k);
                             }
                         }

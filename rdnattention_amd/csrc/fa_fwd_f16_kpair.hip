@@ -30,7 +30,8 @@
 // classes, and (up to D = 192) a persistent grid.
 //
 // K/V tiles move HBM -> LDS by DMA (buffer_load ... lds), two rows per
-// instruction, issued by group B in its softmax phase; the row-pair LDS layout
+// instruction, issued in the softmax phases (K tiles by group B, V tiles by
+// group A); the row-pair LDS layout
 // (KPCfg) keeps both operand reads free of bank conflicts.  The issuing wave
 // waits on each DMA instruction (~70 cycles with four waves issuing), whatever
 // its size, so the instruction count sets the cost: one row per DMA cost more
@@ -77,13 +78,16 @@ struct KPCfg {
     static constexpr int DA = 32 * ((D + 63) / 64); // O^T columns of half 0
     static constexpr int DB = D - DA;               // ... of half 1
     static constexpr int KCH = D / 8;               // 16-byte chunks per K/V row
-    // Staging: by DMA from D = 224 (group-B wave w moves row pairs 8w .. 8w +
-    // 7 of each K and V tile), below through registers (each group its 32
+    // Staging: by DMA from D = 224 (wave w of group B moves row pairs 8w ..
+    // 8w + 7 of each K tile, of group A of each V tile), below through registers (each group its 32
     // rows, RPI rows per pass, CT passes), which measured faster there: a DMA
     // instruction costs the same however few of its lanes a short row fills
     static constexpr bool DMA = D >= 224;
     static constexpr int DMA_PAIRS = kKPBN / 2 / 4;
-    static constexpr int NDMA = 2 * DMA_PAIRS; // DMA instructions per group-B wave per tile
+    static constexpr int NDMA = 2 * DMA_PAIRS; // DMA instructions of a K and V tile pair per wave
+    // K tiles by group B, V tiles by group A in its own softmax phase (else
+    // both by group B)
+    static constexpr bool DMA_SPLIT = true;
     static constexpr int RPI = (256 / KCH) & ~1;
     static constexpr int CT = (32 + RPI - 1) / RPI;
     static_assert(DMA || RPI * KCH <= 256, "register staging: one chunk per thread and pass");
@@ -143,8 +147,8 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
     // instruction per row pair: lane i moves global chunk c of row 2j + i / 32
     // to LDS byte 16 i of the pair, c = i for i < 32 and c = (i - 32 + 24) mod
     // 32 above (the odd row's rotation); lanes whose chunk lies past the row
-    // idle.  Only group B issues them, in its softmax phase: wave w of the
-    // group moves pairs 8w .. 8w + 7 of each K and V tile.  The pair's row
+    // idle.  They are issued in the softmax phases: wave w of group B moves
+    // pairs 8w .. 8w + 7 of each K tile, wave w of group A those of each V tile.  The pair's row
     // offset is the instruction's scalar offset, its LDS address M0.
     const uint32_t dma_j0 = (uint32_t)__builtin_amdgcn_readfirstlane((wave & 3) * C::DMA_PAIRS);
     const int dma_c = lane < 32 ? lane : ((lane + 24) & 31);
@@ -229,7 +233,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         // 2 masked): both halves of a pair share rows, so they share classes
         const TileClasses tcls = wave_active ? tile_classes<kKPBN>(p.mask, q0, q_hi) : TileClasses{1, 0, 1, 0};
 
-        // Group B sets up pair x = 0, 1, 2, ... in order: K(x) and V(x - 1).
+        // Each group sets up pair x = 0, 1, 2, ... in order: K(x) and V(x - 1).
         // The tile addresses advance by one stride per pair and step back n
         // strides where the walk wraps (unsigned arithmetic: tiles past the
         // walk, and V tile -1 of pair 0, are never read; their num_records is
@@ -279,6 +283,13 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
 #pragma unroll
             for (int k = 0; k < C::NDMA; k++) {
                 dma_issue(d, k);
+            }
+        };
+        // the K half (even k) or the V half (odd k) of a tile pair
+        auto dma_half = [&](const DmaPair& d, int parity) {
+#pragma unroll
+            for (int k = 0; k < C::NDMA; k += 2) {
+                dma_issue(d, k + parity);
             }
         };
 
@@ -599,29 +610,45 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         __syncthreads();
         // Group A: M(i) in phase 2i, V(i) in phase 2i + 1; group B one phase
         // later.  K(i) is read in phases 2i and 2i + 1, V(i) in 2i + 2 and
-        // 2i + 3.  DMA: group B issues K(i + 2) (K(i)'s slot) and V(i + 1)
-        // (V(i - 1)'s) at the start of its V(i), in phase 2i + 2, and waits for
-        // them at the end of its M(i + 1), phase 2i + 3; K(1) and V(0) in phase
-        // 0.  Registers: each group stores pair i + 1 (A) or i + 2 (B) and
+        // 2i + 3.  DMA: group B issues K(i + 2) (K(i)'s slot) at the start of
+        // its V(i), in phase 2i + 2, and waits for it at the end of its
+        // M(i + 1), phase 2i + 3 (K(1) in phase 0); group A issues V(i)
+        // (V(i - 2)'s slot, last read in phase 2i - 1) at the start of its
+        // V(i), phase 2i + 1, and waits for it at the end of that phase.  Each
+        // softmax side thus carries 8 DMAs per wave per tile, not 0 and 16
+        // (two-sided window +-2048 + RoPE, B1 H16 S16384 D256: -1.9 %; D224
+        // non-causal -3.8 %).  Registers: each group stores pair i + 1 (A) or i + 2 (B) and
         // loads the next in its V(i).  Both groups pass 2n + 2 barriers after
         // the prologue's.
         if (n > 0) {
             if (grp == 0) {
+                if constexpr (C::DMA && C::DMA_SPLIT) {
+                    (void)dma_pair(0); // the address stepping starts at pair 0
+                }
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     __syncthreads();
                     if constexpr (!C::DMA) {
                         store_pair(i + 1);
                         load_pair(i + 2);
+                    } else if constexpr (C::DMA_SPLIT) {
+                        dma_half(dma_pair(i + 1), 1); // V(i)
                     }
                     phase_v(i);
+                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // V(i) landed
+                    }
                     __syncthreads();
                 }
                 phase_m(n);
                 __syncthreads();
                 __syncthreads();
             } else {
-                if constexpr (C::DMA) {
+                if constexpr (C::DMA && C::DMA_SPLIT) {
+                    if (1 < n) {
+                        dma_half(dma_pair(1), 0);
+                    }
+                } else if constexpr (C::DMA) {
                     dma_all(dma_pair(1));
                 } else {
                     store_pair(1);
@@ -634,7 +661,11 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
                     }
                     __syncthreads();
-                    if constexpr (C::DMA) {
+                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                        if (i + 2 < n) {
+                            dma_half(dma_pair(i + 2), 0); // K(i + 2)
+                        }
+                    } else if constexpr (C::DMA) {
                         if (i + 2 <= n) {
                             dma_all(dma_pair(i + 2));
                         }
