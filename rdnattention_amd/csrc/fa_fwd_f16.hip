@@ -626,7 +626,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     if constexpr (C::DMA) {
-                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed (and V(i) without the split)
                     }
                     __syncthreads();
                     if constexpr (C::DMA) {

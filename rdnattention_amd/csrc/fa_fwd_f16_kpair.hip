@@ -658,7 +658,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     if constexpr (C::DMA) {
-                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1), V(i) landed
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed (and V(i) without the split)
                     }
                     __syncthreads();
                     if constexpr (C::DMA && C::DMA_SPLIT) {
