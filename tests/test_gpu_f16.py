@@ -286,6 +286,23 @@ def test_pair_kernel_few_key_tiles(gpu, oracle_lib, d, sq, sk):
     assert_f16_parity(out.float().cpu().numpy(), ref, f"few_tiles d{d} {sq}x{sk}")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk", [(70, 20), (40, 64), (130, 100), (200, 150)])
+@pytest.mark.parametrize("d", [128, 224, 256])
+def test_dma_staged_kernels_few_key_tiles(gpu, oracle_lib, d, sq, sk, causal):
+    """The kernels whose K/V tiles arrive by DMA from both groups (D = 128:
+    the ping-pong kernel; D = 224, 256: the key-pair kernel) with one, two and
+    three 64-key tiles, full and partial: group B's prologue and phase-0 K
+    DMAs, group A's first V DMA and the skipped in-loop K issues near the
+    end; causal with Sq > Sk leaves rows that see no key."""
+    q, k, v = seeded_inputs(23, 1, 4, 2, sq, sk, d)
+    out = torch.full_like(q, float("nan"), device=gpu)
+    assert forward_raw(q.to(gpu), k.to(gpu), v.to(gpu), out, causal, -1) == 0
+    torch.cuda.synchronize()
+    ref = reference_f16(q, k, v, causal, -1)
+    assert_f16_parity(out.float().cpu().numpy(), ref, f"dma_few_tiles d{d} {sq}x{sk} causal={causal}")
+
+
 @pytest.mark.parametrize("d,s,window", [(256, 2048, 1024), (512, 1024, 1024), (416, 640, 256)])
 def test_large_head_window_rope_slice(gpu, oracle_lib, d, s, window):
     """The large-head window workloads (two-sided window, RoPE, N(0, 0.5)) at
