@@ -85,9 +85,6 @@ struct PPCfg {
     // moved by 64 b), and the 8-row transpose reads of V fall twice on each
     // 64-byte quarter (group j at 64 j, row b's chunk quad moved by b).
     static constexpr bool DMA = D == 128;
-    // K tiles by group B, V tiles by group A in its own softmax phase (else
-    // both by group B)
-    static constexpr bool DMA_SPLIT = true;
     static constexpr int PSK = 520;
     static constexpr int PSV = 544;
     static constexpr int TILE_K = DMA ? (kBN / 4) * PSK : kBN * LDK;
@@ -580,7 +577,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         // Both groups pass 2n + 2 barriers; group B starts one phase late.
         if (n > 0) {
             if (grp == 0) {
-                if constexpr (C::DMA && C::DMA_SPLIT) {
+                if constexpr (C::DMA) {
                     (void)dma_pair(0); // the address stepping starts at pair 0
                 }
                 for (int i = 0; i < n; i++) {
@@ -589,7 +586,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                     if constexpr (!C::DMA) {
                         store_pair(i + 1);
                         load_pair(i + 2);
-                    } else if constexpr (C::DMA_SPLIT) {
+                    } else {
                         // V(i) into V(i - 2)'s slot, last read in phase 2i - 1;
                         // first read in phase 2i + 2
                         const DmaPair d = dma_pair(i + 1);
@@ -599,7 +596,7 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                         }
                     }
                     phase_v(i);
-                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                    if constexpr (C::DMA) {
                         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // V(i) landed
                     }
                     __syncthreads();
@@ -611,10 +608,10 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 // DMA: group B issues K(i + 2) at the start of its V(i) and
                 // waits for it at the end of its M(i + 1); K(1) in phase 0
                 if constexpr (C::DMA) {
-                    if (!C::DMA_SPLIT || 1 < n) {
+                    if (1 < n) {
                         const DmaPair d1 = dma_pair(1);
 #pragma unroll
-                        for (int k = 0; k < 8; k += C::DMA_SPLIT ? 2 : 1) {
+                        for (int k = 0; k < 8; k += 2) {
                             dma_issue(d1, k);
                         }
                     }
@@ -626,14 +623,14 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     if constexpr (C::DMA) {
-                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed (and V(i) without the split)
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed
                     }
                     __syncthreads();
                     if constexpr (C::DMA) {
-                        if (i + 2 < n || (!C::DMA_SPLIT && i + 2 == n)) {
+                        if (i + 2 < n) {
                             const DmaPair d = dma_pair(i + 2);
 #pragma unroll
-                            for (int k = 0; k < 8; k += C::DMA_SPLIT ? 2 : 1) {
+                            for (int k = 0; k < 8; k += 2) {
                                 dma_issue(d, k);
                             }
                         }

@@ -85,9 +85,6 @@ struct KPCfg {
     static constexpr bool DMA = D >= 224;
     static constexpr int DMA_PAIRS = kKPBN / 2 / 4;
     static constexpr int NDMA = 2 * DMA_PAIRS; // DMA instructions of a K and V tile pair per wave
-    // K tiles by group B, V tiles by group A in its own softmax phase (else
-    // both by group B)
-    static constexpr bool DMA_SPLIT = true;
     static constexpr int RPI = (256 / KCH) & ~1;
     static constexpr int CT = (32 + RPI - 1) / RPI;
     static_assert(DMA || RPI * KCH <= 256, "register staging: one chunk per thread and pass");
@@ -279,13 +276,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 }
             }
         };
-        auto dma_all = [&](const DmaPair& d) {
-#pragma unroll
-            for (int k = 0; k < C::NDMA; k++) {
-                dma_issue(d, k);
-            }
-        };
-        // the K half (even k) or the V half (odd k) of a tile pair
+        // the K half (even k, group B) or the V half (odd k, group A) of a tile pair
         auto dma_half = [&](const DmaPair& d, int parity) {
 #pragma unroll
             for (int k = 0; k < C::NDMA; k += 2) {
@@ -622,7 +613,7 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
         // the prologue's.
         if (n > 0) {
             if (grp == 0) {
-                if constexpr (C::DMA && C::DMA_SPLIT) {
+                if constexpr (C::DMA) {
                     (void)dma_pair(0); // the address stepping starts at pair 0
                 }
                 for (int i = 0; i < n; i++) {
@@ -631,11 +622,11 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                     if constexpr (!C::DMA) {
                         store_pair(i + 1);
                         load_pair(i + 2);
-                    } else if constexpr (C::DMA_SPLIT) {
+                    } else {
                         dma_half(dma_pair(i + 1), 1); // V(i)
                     }
                     phase_v(i);
-                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                    if constexpr (C::DMA) {
                         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // V(i) landed
                     }
                     __syncthreads();
@@ -644,12 +635,10 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 __syncthreads();
                 __syncthreads();
             } else {
-                if constexpr (C::DMA && C::DMA_SPLIT) {
+                if constexpr (C::DMA) {
                     if (1 < n) {
                         dma_half(dma_pair(1), 0);
                     }
-                } else if constexpr (C::DMA) {
-                    dma_all(dma_pair(1));
                 } else {
                     store_pair(1);
                     load_pair(2);
@@ -658,16 +647,12 @@ __device__ __forceinline__ void kpair_half(const PrefillParams& p, char* smem, c
                 for (int i = 0; i < n; i++) {
                     phase_m(i);
                     if constexpr (C::DMA) {
-                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed (and V(i) without the split)
+                        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // K(i + 1) landed
                     }
                     __syncthreads();
-                    if constexpr (C::DMA && C::DMA_SPLIT) {
+                    if constexpr (C::DMA) {
                         if (i + 2 < n) {
                             dma_half(dma_pair(i + 2), 0); // K(i + 2)
-                        }
-                    } else if constexpr (C::DMA) {
-                        if (i + 2 <= n) {
-                            dma_all(dma_pair(i + 2));
                         }
                     } else {
                         store_pair(i + 2);
