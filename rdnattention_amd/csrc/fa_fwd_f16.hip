@@ -144,9 +144,9 @@ __global__ __launch_bounds__(kPPThreads, 1) void fa_fwd_f16_pp(PrefillParams p) 
         clv[it] = ok ? row * C::LDV + 8 * ch : -1;
     }
     // DMA staging (PPCfg::DMA): wave w of group B (K) or A (V) moves 4-row
-    // groups 4w .. 4w + 3 of each tile, lane i global chunk (i % 16) ^ 4 (i / 16) of row
-    // 4j + i / 16 to LDS byte 16 i of group j; the group's row offset is the
-    // instruction's scalar offset, its LDS address M0.
+    // groups 4w .. 4w + 3 of each tile, lane i global chunk (i % 16) ^ 4 (i /
+    // 16) of row 4j + i / 16 to LDS byte 16 i of group j; the group's row
+    // offset is the instruction's scalar offset, its LDS address M0.
     const uint32_t dma_j0 = (uint32_t)__builtin_amdgcn_readfirstlane((wave & 3) * 4);
     const uint32_t dma_c = (uint32_t)((lane & 15) ^ (4 * (lane >> 4)));
     const uint32_t dma_vk = (uint32_t)(lane >> 4) * (uint32_t)(p.k_ss * 2) + 16u * dma_c;
